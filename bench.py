@@ -1,0 +1,223 @@
+"""Headline benchmark: batched GDN decode at B=128 on one MI355X.
+
+Workload: one step = gdn_decode_raw over B=128 rows of a
+Qwen3.5-9B-shaped GDN layer (32 value heads, 16 key heads, 128x128 fp16 state
+per head, fp32 recurrence math, in-kernel gates from bf16 raw projections) on
+a 160-slot fp16 state pool addressed through a random permutation of 128
+distinct slots. Synthetic inputs, seeded.
+
+Timing: K steps are captured in one hipGraph and replayed once between two
+synchronisations, timed with events on the stream the kernels run on. The
+default is COLD: step i runs on pool i % P, with P pools totalling > 1 GiB, so
+neither the L2s nor the 256 MB Infinity Cache hold a state slab when it is
+revisited (a single 160 MiB pool would fit and report above-HBM figures). The
+HOT figure (one pool reused) is reported beside it, labelled.
+
+Roofline: the decode is HBM-bound. Algorithmic bytes per step are
+274,744,064 (state read + write 268,435,456; q/k/v/y 6,291,456; bf16 gates
+16,384; A/dt_bias/slot map 768). achieved = bytes / mean step time; peak 8 TB/s.
+
+cpu_baseline: the CPU oracle (oracle/gdn_oracle.c, a scalar port of the same
+recurrence, one thread) timed on a bounded sample of rows of the same
+workload and scaled to steps/s at B=128.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+H, G, D = 32, 16, 128
+B, SLOTS = 128, 160
+STATE_BYTES = B * H * D * D * 2 * 2                 # fp16 read + write
+ACT_BYTES = B * (2 * G * D + 2 * H * D) * 4         # q, k, v in; y out (fp32)
+GATE_BYTES = B * H * 2 * 2                          # a_raw, b_raw bf16
+CONST_BYTES = 2 * H * 4 + B * 4                     # A, dt_bias, slot map
+STEP_BYTES = STATE_BYTES + ACT_BYTES + GATE_BYTES + CONST_BYTES
+HBM_PEAK_GBS = 8000.0
+COLD_BYTES = 1.1 * 2 ** 30
+TRAFFIC_FILE = ROOT / "profiles" / "gdn_decode_b128_traffic.json"
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=512)
+    ap.add_argument("--warmup", type=int, default=32)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="budget for the CPU-oracle baseline sample")
+    return ap.parse_args()
+
+
+def make_workload(torch, n_pools, seed=0):
+    dev = "cuda"
+    g = torch.Generator(device=dev).manual_seed(seed)
+    pools, slot_maps, inputs = [], [], []
+    for p in range(n_pools):
+        pools.append((torch.randn(SLOTS, H, D, D, generator=g, device=dev) * 0.02).half())
+        perm = torch.randperm(SLOTS, generator=torch.Generator().manual_seed(seed + p))
+        slot_maps.append(perm[:B].to(torch.int32).to(dev))
+        inputs.append(dict(
+            q=torch.randn(B, G, D, generator=g, device=dev),
+            k=torch.randn(B, G, D, generator=g, device=dev),
+            v=torch.randn(B, H, D, generator=g, device=dev),
+            a=torch.randn(B, H, generator=g, device=dev).to(torch.bfloat16),
+            b=torch.randn(B, H, generator=g, device=dev).to(torch.bfloat16),
+            y=torch.empty(B, H, D, device=dev),
+        ))
+    A = -torch.exp(torch.rand(H, generator=g, device=dev) * 2)
+    dt_bias = torch.rand(H, generator=g, device=dev) * 2 - 1
+    return pools, slot_maps, inputs, A, dt_bias
+
+
+def time_steps(torch, kern, work, steps, warmup):
+    """Capture `steps` decode launches (step i on pool i % P) in one graph,
+    replay it once between synchronisations; returns seconds for all steps."""
+    pools, slot_maps, inputs, A, dtb = work
+    P = len(pools)
+
+    def launch(i):
+        p = i % P
+        x = inputs[p]
+        kern.gdn_decode_raw(pools[p], slot_maps[p], x["q"], x["k"], x["v"], x["a"], x["b"], A,
+                            dtb, x["y"])
+
+    for i in range(warmup):
+        launch(i)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(steps):
+            launch(i)
+    graph.replay()                       # untimed: first replay uploads the graph
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / 1e3
+
+
+def copy_bandwidth(torch, nbytes=2 ** 30):
+    src = torch.empty(nbytes // 2, dtype=torch.float16, device="cuda")
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = 10
+    start.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    end.record()
+    torch.cuda.synchronize()
+    secs = start.elapsed_time(end) / 1e3 / reps
+    del src, dst
+    return 2 * nbytes / secs / 1e9
+
+
+def cpu_baseline(budget_s):
+    """Time the scalar CPU oracle on whole rows of the workload (fp16 state
+    emulated), one thread; scale to steps/s at B=128."""
+    import numpy as np
+
+    import oracle
+
+    rng = np.random.default_rng(0)
+    A = -np.exp(rng.uniform(0, 2, H)).astype(np.float32)
+    dtb = rng.uniform(-1, 1, H).astype(np.float32)
+
+    def one_row():
+        pool = (rng.standard_normal((1, H, D, D)) * 0.02).astype(np.float16)
+        q = rng.standard_normal((1, G, D)).astype(np.float32)
+        k = rng.standard_normal((1, G, D)).astype(np.float32)
+        v = rng.standard_normal((1, H, D)).astype(np.float32)
+        a = oracle.bf16_bits(rng.standard_normal((1, H)).astype(np.float32))
+        b = oracle.bf16_bits(rng.standard_normal((1, H)).astype(np.float32))
+        t = time.perf_counter()
+        al, be = oracle.gdn_gates(a, b, A, dtb, "bf16")
+        oracle.gdn_decode(pool, [0], q, k, v, al, be, "f16")
+        return time.perf_counter() - t
+
+    one_row()
+    rows, spent = 0, 0.0
+    while spent < budget_s and rows < 4 * B:
+        spent += one_row()
+        rows += 1
+    per_row = spent / rows
+    return {"value": 1.0 / (per_row * B), "unit": "steps/s", "cores": 1, "kind": "port",
+            "sample": f"{rows} rows of the B=128 step (32 heads, fp16 state emulated, bf16 "
+                      f"gates) on the scalar C oracle, {spent:.1f} s, scaled x{B}/rows",
+            "host_cpus": os.cpu_count()}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU: this build has no multi-GPU path and the box has "
+              f"one GPU (asked for --gpus {args.gpus})", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from braid_amd.kernels.loader import load_gdn
+
+    kern = load_gdn()
+    n_cold = max(2, math.ceil(COLD_BYTES / (SLOTS * H * D * D * 2)))
+    work = make_workload(torch, n_cold)
+    t_cold = time_steps(torch, kern, work, args.steps, args.warmup)
+    hot_work = tuple([x[:1] for x in work[:3]] + list(work[3:]))
+    t_hot = time_steps(torch, kern, hot_work, args.steps, args.warmup)
+    del work, hot_work
+    torch.cuda.empty_cache()
+    copy_gbs = copy_bandwidth(torch)
+
+    step_s = t_cold / args.steps
+    achieved = STEP_BYTES / step_s / 1e9
+    traffic = None
+    if TRAFFIC_FILE.exists():
+        traffic = json.loads(TRAFFIC_FILE.read_text()).get("hbm_bytes_per_launch")
+    out = {
+        "metric": "GDN decode steps/s and achieved HBM GB/s (% of peak) at B=128, 1 MI355X",
+        "value": round(args.steps / t_cold, 2),
+        "unit": "steps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_s * 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "config1: batched GDN decode (gdn_decode_raw), B=128, "
+                               "160-slot fp16 pool, permuted slots, cold pools",
+                   "batch": B, "value_heads": H, "key_heads": G, "state": "128x128 fp16",
+                   "gates": "in-kernel from bf16 raw", "cold_pools": n_cold},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic},
+        "achieved_gbs": round(achieved, 1),
+        "hbm_frac": round(achieved / HBM_PEAK_GBS, 4),
+        "hot_steps_per_s": round(args.steps / t_hot, 2),
+        "hot_achieved_gbs": round(STEP_BYTES / (t_hot / args.steps) / 1e9, 1),
+        "copy_gbs": round(copy_gbs, 1),
+        "bytes_per_step": STEP_BYTES,
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,84 @@
+"""Build libbraid_gdn.so (the C-ABI kernel library) for gfx950 with hipcc.
+
+Run as ``python -m braid_amd.build``; ``__graft_entry__.build()`` calls
+:func:`build`. The library lands in-tree at ``braid_amd/libbraid_gdn.so`` so it
+travels with the source tree; nothing is installed.
+
+Flags that matter for numerics:
+
+* no fast-math: division and sqrt stay correctly rounded and ``expf`` /
+  ``log1pf`` stay the accurate device-library routines, which is what torch's
+  own elementwise kernels use (the in-kernel gates are compared bitwise
+  against torch's spelling);
+* ``-ffp-contract=off``: nothing is fused behind the source's back; every
+  fused multiply-add in the kernels is an explicit ``fmaf``, so the
+  decode and prefill kernels provably run the same operations;
+* packed-fp32 instructions disabled (``-packed-fp32-ops``).
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+CSRC = PKG / "csrc"
+ROOT = PKG.parent
+LIB = PKG / "libbraid_gdn.so"
+OBJ_DIR = PKG / "_build"
+
+SOURCES = ["capi_common.cpp", "gdn_scan.hip", "conv1d_decode.hip", "quant_act.hip"]
+
+ARCH = os.environ.get("BRAID_OFFLOAD_ARCH", "gfx950")
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc"):
+        if cand and Path(cand).exists():
+            return cand
+    return "hipcc"
+
+
+def common_flags() -> list[str]:
+    return [
+        "-O3", "-std=c++17", "-fPIC",
+        f"--offload-arch={ARCH}",
+        "-ffp-contract=off",
+        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        "-I", str(ROOT / "include"),
+        "-Wall", "-Wno-unused-result",
+    ]
+
+
+def _compile(src: str) -> Path:
+    OBJ_DIR.mkdir(exist_ok=True)
+    out = OBJ_DIR / (Path(src).stem + ".o")
+    lang = ["-x", "hip"] if src.endswith(".hip") else []
+    cmd = [hipcc(), *common_flags(), *lang, "-c", str(CSRC / src), "-o", str(out)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {src}:\n{' '.join(cmd)}\n{r.stdout}{r.stderr}")
+    return out
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile every source and link the shared library. Always rebuilds."""
+    with ThreadPoolExecutor(max_workers=min(4, len(SOURCES))) as ex:
+        objs = list(ex.map(_compile, SOURCES))
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs),
+           "-o", str(tmp)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link failed:\n{' '.join(cmd)}\n{r.stdout}{r.stderr}")
+    os.replace(tmp, LIB)
+    if verbose:
+        print(f"built {LIB}")
+    return LIB
+
+
+if __name__ == "__main__":
+    build(verbose=True)
+    sys.exit(0)

@@ -1,0 +1,35 @@
+// Host-side helpers shared by the C-ABI entry points: thread-local error text,
+// HIP status checks and the slot-map validation every pool entry performs.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../../include/braid_gdn.h"
+
+namespace braid {
+
+// Records `msg` as this thread's last error and returns `code`.
+int fail(int code, const std::string& msg);
+// Clears the last error and returns BRAID_OK.
+int ok();
+
+// HIP call wrapper: on failure records "<what>: <hip error string>".
+int hip_status(hipError_t e, const char* what);
+
+// True when `stream` is capturing a graph (then no host round trip is legal).
+// Returns a braid status through `status`.
+bool stream_capturing(hipStream_t stream, int* status);
+
+// Copies slot_idx[0..B) to the host (skipped while capturing) and checks every
+// entry lies in [0, n_slots); with `distinct`, also that no slot repeats.
+// Message fragments follow braid/kernels/csrc/gdn_decode.cu:289-296:
+// "... is out of range [0, n)" and "duplicate slot ... must be distinct".
+int validate_slots(const int32_t* slot_idx, int B, int64_t n_slots, bool distinct,
+                   hipStream_t stream);
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace braid

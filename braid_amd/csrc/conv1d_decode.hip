@@ -1,0 +1,132 @@
+// Batched slotted causal depthwise conv1d, one decode step, SiLU fused.
+//
+// Reference behaviour: braid/kernels/csrc/conv1d_decode.cu:40-75. Per channel
+// c of batch row b, with the window st = conv_pool[slot_idx[b], c, 0..K) holding
+// the last K pre-conv inputs (oldest first, K contiguous per channel):
+//   w   = (st[1], ..., st[K-1], x[b, c])     window slides left, new value last
+//   st <- w
+//   out[b, c] = SiLU(sum_i w[i] * weight[c, i] + bias[c])
+// SiLU applies to every channel (Q, K and V alike); bias is added after the dot
+// and before the activation.
+//
+// One thread per channel. At K = 4 a channel's window is one 16-byte fp32
+// vector, so the pool read, the pool write and the weight read are single
+// 128-bit accesses and a wave moves 1 KiB per instruction.
+#include "capi_common.h"
+
+namespace braid {
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float conv_widen(float x) { return x; }
+__device__ __forceinline__ float conv_widen(uint16_t bf16) {
+  return __uint_as_float((uint32_t)bf16 << 16);
+}
+
+__device__ __forceinline__ float silu(float a) { return a / (1.f + expf(-a)); }
+
+template <int K, class XT>
+__global__ void __launch_bounds__(256)
+conv1d_decode_kernel(float* __restrict__ conv_pool, const int* __restrict__ slot_idx,
+                     const XT* __restrict__ x, const float* __restrict__ weight,
+                     const float* __restrict__ bias, float* __restrict__ out, int C) {
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= C) return;
+  const int b = blockIdx.y;
+  const int slot = slot_idx[b];
+  float* st = conv_pool + ((size_t)slot * C + c) * K;
+  const float* wr = weight + (size_t)c * K;
+
+  float w[K], wt[K];
+  if constexpr (K == 4) {
+    const f32x4 s4 = *reinterpret_cast<const f32x4*>(st);
+    const f32x4 w4 = *reinterpret_cast<const f32x4*>(wr);
+    w[0] = s4[1];
+    w[1] = s4[2];
+    w[2] = s4[3];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) wt[i] = w4[i];
+  } else {
+#pragma unroll
+    for (int i = 0; i < K - 1; ++i) w[i] = st[i + 1];
+#pragma unroll
+    for (int i = 0; i < K; ++i) wt[i] = wr[i];
+  }
+  w[K - 1] = conv_widen(x[(size_t)b * C + c]);
+
+  float acc = w[0] * wt[0];
+#pragma unroll
+  for (int i = 1; i < K; ++i) acc = fmaf(w[i], wt[i], acc);
+  if (bias != nullptr) acc += bias[c];
+
+  if constexpr (K == 4) {
+    f32x4 s4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s4[i] = w[i];
+    *reinterpret_cast<f32x4*>(st) = s4;
+  } else {
+#pragma unroll
+    for (int i = 0; i < K; ++i) st[i] = w[i];
+  }
+  out[(size_t)b * C + c] = silu(acc);
+}
+
+template <class XT>
+int launch(int K, float* conv_pool, const int32_t* slot_idx, int B, const XT* x,
+           const float* weight, const float* bias, float* out, int C, hipStream_t stream) {
+  const int threads = 256;
+  const dim3 grid((unsigned)((C + threads - 1) / threads), (unsigned)B);
+  switch (K) {
+    case 2:
+      conv1d_decode_kernel<2, XT><<<grid, threads, 0, stream>>>(conv_pool, slot_idx, x, weight,
+                                                                bias, out, C);
+      break;
+    case 3:
+      conv1d_decode_kernel<3, XT><<<grid, threads, 0, stream>>>(conv_pool, slot_idx, x, weight,
+                                                                bias, out, C);
+      break;
+    case 4:
+      conv1d_decode_kernel<4, XT><<<grid, threads, 0, stream>>>(conv_pool, slot_idx, x, weight,
+                                                                bias, out, C);
+      break;
+    default:
+      conv1d_decode_kernel<8, XT><<<grid, threads, 0, stream>>>(conv_pool, slot_idx, x, weight,
+                                                                bias, out, C);
+      break;
+  }
+  const int st = hip_status(hipGetLastError(), "launching conv1d_decode_kernel");
+  return st != BRAID_OK ? st : ok();
+}
+
+}  // namespace
+}  // namespace braid
+
+using namespace braid;
+
+extern "C" int braid_conv1d_decode(float* conv_pool, int64_t n_slots, int C, int K,
+                                   const int32_t* slot_idx, int B, const void* x, int x_dtype,
+                                   const float* weight, const float* bias, float* out,
+                                   void* stream_) {
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  if (K != 2 && K != 3 && K != 4 && K != 8)
+    return fail(BRAID_EINVAL,
+                "conv_kernel " + std::to_string(K) + " is not instantiated (have 2, 3, 4, 8)");
+  if (x_dtype != BRAID_F32 && x_dtype != BRAID_BF16)
+    return fail(BRAID_EINVAL, "x must be fp32 or bf16 (the activation dtypes braid runs)");
+  if (C <= 0 || B < 0 || n_slots <= 0)
+    return fail(BRAID_EINVAL, "conv_pool must be [S_max, C, K] with S_max, C > 0");
+  if (B == 0) return ok();
+  if (conv_pool == nullptr || slot_idx == nullptr || x == nullptr || weight == nullptr ||
+      out == nullptr)
+    return fail(BRAID_EINVAL, "conv_pool/slot_idx/x/weight/out must be non-null");
+  if (K == 4 && (!aligned16(conv_pool) || !aligned16(weight)))
+    return fail(BRAID_EINVAL, "conv_pool and weight must be 16-byte aligned at K = 4");
+  const int st = validate_slots(slot_idx, B, n_slots, false, stream);
+  if (st != BRAID_OK) return st;
+  if (x_dtype == BRAID_F32)
+    return launch(K, conv_pool, slot_idx, B, static_cast<const float*>(x), weight, bias, out, C,
+                  stream);
+  return launch(K, conv_pool, slot_idx, B, static_cast<const uint16_t*>(x), weight, bias, out, C,
+                stream);
+}

@@ -1,0 +1,299 @@
+// Batched Gated DeltaNet decode step and chunk prefill scan for gfx950.
+//
+// Both kernels launch one 256-thread workgroup (four waves, one per 32-column
+// panel) per (batch row, value head) tile and run the same per-token device
+// function, braid::gdn_token. Decode loads the tile from the slot-indexed pool,
+// runs one token and stores it back; prefill loads it once, runs T tokens with
+// the tile resident in registers (in the pool's storage type) and stores it
+// once. Reference behaviour: braid/kernels/csrc/gdn_decode.cu:156-272 (decode)
+// and :467-551 (prefill); entry-point contracts :313-441 and :553-699.
+#include "capi_common.h"
+#include "gdn_tile.h"
+
+namespace braid {
+namespace {
+
+template <class Tag>
+struct Storage;
+template <>
+struct Storage<F32> { using T = float; };
+template <>
+struct Storage<F16> { using T = uint16_t; };
+template <>
+struct Storage<BF16> { using T = uint16_t; };
+
+template <class Tag, class Gates>
+__global__ void __launch_bounds__(kTileThreads)
+gdn_decode_kernel(typename Storage<Tag>::T* __restrict__ pool,
+                  const int* __restrict__ slot_idx,
+                  const float* __restrict__ q, const float* __restrict__ k,
+                  const float* __restrict__ v, Gates gates, float* __restrict__ y,
+                  int H, int heads_per_group, long q_row, long k_row, long v_row) {
+  using ST = typename Storage<Tag>::T;
+  const int b = blockIdx.x / H;
+  const int h = blockIdx.x - b * H;
+  const int g = h / heads_per_group;
+  const LaneMap L(threadIdx.x);
+
+  // The slot comes from device memory, so one captured graph serves any slot
+  // assignment (gdn_decode.cu:230-236).
+  const int slot = slot_idx[b];
+  ST* tile = pool + ((size_t)slot * H + h) * (kSS * kHD) + L.col0;
+
+  // Issue the whole tile's loads first; the norms and gates below overlap them.
+  Row8<Tag> S[kRowsPerLane];
+#pragma unroll
+  for (int i = 0; i < kRowsPerLane; ++i) S[i].load(tile + (size_t)L.row(i) * kHD);
+
+  float vv[8];
+  load8(v + (size_t)b * v_row + (size_t)h * kHD + L.col0, vv);
+  QK qk;
+  normalize_qk(L, q + (size_t)b * q_row + (size_t)g * kSS,
+               k + (size_t)b * k_row + (size_t)g * kSS, qk);
+  float a, bt;
+  gates.get(b, h, 0, H, 1, a, bt);
+
+  float yy[8];
+  gdn_token<Tag>(S, qk, vv, a, bt, yy);
+
+#pragma unroll
+  for (int i = 0; i < kRowsPerLane; ++i) S[i].store(tile + (size_t)L.row(i) * kHD);
+  if (L.rg == 0) store8(y + ((size_t)b * H + h) * kHD + L.col0, yy);
+}
+
+template <class Tag, class Gates>
+__global__ void __launch_bounds__(kTileThreads)
+gdn_prefill_kernel(typename Storage<Tag>::T* __restrict__ pool,
+                   const int* __restrict__ slot_idx,
+                   const float* __restrict__ q, const float* __restrict__ k,
+                   const float* __restrict__ v, Gates gates, float* __restrict__ y,
+                   int H, int G, int heads_per_group, int T) {
+  using ST = typename Storage<Tag>::T;
+  const int b = blockIdx.x / H;
+  const int h = blockIdx.x - b * H;
+  const int g = h / heads_per_group;
+  const LaneMap L(threadIdx.x);
+
+  const int slot = slot_idx[b];
+  ST* tile = pool + ((size_t)slot * H + h) * (kSS * kHD) + L.col0;
+
+  Row8<Tag> S[kRowsPerLane];
+#pragma unroll
+  for (int i = 0; i < kRowsPerLane; ++i) S[i].load(tile + (size_t)L.row(i) * kHD);
+
+  for (int t = 0; t < T; ++t) {
+    const size_t bt_idx = (size_t)b * T + t;
+    float vv[8];
+    load8(v + (bt_idx * H + h) * kHD + L.col0, vv);
+    QK qk;
+    normalize_qk(L, q + (bt_idx * G + g) * kSS, k + (bt_idx * G + g) * kSS, qk);
+    float a, bt;
+    gates.get(b, h, t, H, T, a, bt);
+    float yy[8];
+    gdn_token<Tag>(S, qk, vv, a, bt, yy);
+    if (L.rg == 0) store8(y + (bt_idx * H + h) * kHD + L.col0, yy);
+  }
+
+#pragma unroll
+  for (int i = 0; i < kRowsPerLane; ++i) S[i].store(tile + (size_t)L.row(i) * kHD);
+}
+
+// ---------------------------------------------------------------------------
+// Host-side checks shared by the four entry points.
+
+int check_common(void* pool, int pool_dtype, int64_t n_slots, int H, int G, int SS, int HD,
+                 const int32_t* slot_idx, int B) {
+  if (pool_dtype != BRAID_F32 && pool_dtype != BRAID_F16 && pool_dtype != BRAID_BF16)
+    return fail(BRAID_EINVAL, "state pool must be fp32, fp16 or bf16");
+  if (SS != kSS || HD != kHD) return fail(BRAID_EINVAL, "only SS=HD=128 is instantiated");
+  if (H <= 0 || G <= 0 || H % G != 0)
+    return fail(BRAID_EINVAL, "n_heads must be divisible by n_groups");
+  if (B < 0) return fail(BRAID_EINVAL, "batch must be non-negative");
+  if (n_slots <= 0) return fail(BRAID_EINVAL, "pool must hold at least one slot");
+  if (B > 0 && (pool == nullptr || slot_idx == nullptr))
+    return fail(BRAID_EINVAL, "pool and slot_idx must be non-null");
+  if (!aligned16(pool)) return fail(BRAID_EINVAL, "pool must be 16-byte aligned");
+  return BRAID_OK;
+}
+
+int check_rows(const float* p, int64_t row, int64_t inner, const char* name) {
+  if (p == nullptr) return fail(BRAID_EINVAL, std::string(name) + " must be non-null");
+  if (row < inner) return fail(BRAID_EINVAL, std::string(name) + " rows overlap");
+  if (!aligned16(p) || (row % 4) != 0)
+    return fail(BRAID_EINVAL, std::string(name) +
+                                  " must be 16-byte aligned with a row stride that is a "
+                                  "multiple of 4 elements");
+  return BRAID_OK;
+}
+
+int check_act(const void* a_raw, const void* b_raw, int act_dtype, const float* A,
+              const float* dt_bias) {
+  if (act_dtype != BRAID_F32 && act_dtype != BRAID_BF16)
+    return fail(BRAID_EINVAL,
+                "a_raw/b_raw must be fp32 or bf16 (the activation dtypes braid runs)");
+  if (a_raw == nullptr || b_raw == nullptr || A == nullptr || dt_bias == nullptr)
+    return fail(BRAID_EINVAL, "a_raw/b_raw/A/dt_bias must be non-null");
+  return BRAID_OK;
+}
+
+template <class Gates>
+int launch_decode(void* pool, int pool_dtype, const int32_t* slot_idx, int B, int H, int G,
+                  const float* q, int64_t q_row, const float* k, int64_t k_row, const float* v,
+                  int64_t v_row, Gates gates, float* y, hipStream_t stream) {
+  const dim3 grid((unsigned)B * (unsigned)H), block(kTileThreads);
+  const int hpg = H / G;
+  switch (pool_dtype) {
+    case BRAID_F32:
+      gdn_decode_kernel<F32, Gates><<<grid, block, 0, stream>>>(
+          static_cast<float*>(pool), slot_idx, q, k, v, gates, y, H, hpg, q_row, k_row, v_row);
+      break;
+    case BRAID_F16:
+      gdn_decode_kernel<F16, Gates><<<grid, block, 0, stream>>>(
+          static_cast<uint16_t*>(pool), slot_idx, q, k, v, gates, y, H, hpg, q_row, k_row, v_row);
+      break;
+    default:
+      gdn_decode_kernel<BF16, Gates><<<grid, block, 0, stream>>>(
+          static_cast<uint16_t*>(pool), slot_idx, q, k, v, gates, y, H, hpg, q_row, k_row, v_row);
+      break;
+  }
+  const int st = hip_status(hipGetLastError(), "launching gdn_decode_kernel");
+  return st != BRAID_OK ? st : ok();
+}
+
+template <class Gates>
+int launch_prefill(void* pool, int pool_dtype, const int32_t* slot_idx, int B, int T, int H,
+                   int G, const float* q, const float* k, const float* v, Gates gates,
+                   float* y, hipStream_t stream) {
+  const dim3 grid((unsigned)B * (unsigned)H), block(kTileThreads);
+  const int hpg = H / G;
+  switch (pool_dtype) {
+    case BRAID_F32:
+      gdn_prefill_kernel<F32, Gates><<<grid, block, 0, stream>>>(
+          static_cast<float*>(pool), slot_idx, q, k, v, gates, y, H, G, hpg, T);
+      break;
+    case BRAID_F16:
+      gdn_prefill_kernel<F16, Gates><<<grid, block, 0, stream>>>(
+          static_cast<uint16_t*>(pool), slot_idx, q, k, v, gates, y, H, G, hpg, T);
+      break;
+    default:
+      gdn_prefill_kernel<BF16, Gates><<<grid, block, 0, stream>>>(
+          static_cast<uint16_t*>(pool), slot_idx, q, k, v, gates, y, H, G, hpg, T);
+      break;
+  }
+  const int st = hip_status(hipGetLastError(), "launching gdn_prefill_kernel");
+  return st != BRAID_OK ? st : ok();
+}
+
+int check_dense(const void* p, const char* name) {
+  if (p == nullptr) return fail(BRAID_EINVAL, std::string(name) + " must be non-null");
+  if (!aligned16(p)) return fail(BRAID_EINVAL, std::string(name) + " must be 16-byte aligned");
+  return BRAID_OK;
+}
+
+}  // namespace
+}  // namespace braid
+
+using namespace braid;
+
+#define BRAID_TRY(expr)            \
+  do {                             \
+    const int _st = (expr);        \
+    if (_st != BRAID_OK) return _st; \
+  } while (0)
+
+extern "C" int braid_gdn_decode(void* pool, int pool_dtype, int64_t n_slots, int H, int G,
+                                int SS, int HD, const int32_t* slot_idx, int B, const float* q,
+                                int64_t q_row, const float* k, int64_t k_row, const float* v,
+                                int64_t v_row, const float* alpha, const float* beta, float* y,
+                                void* stream_) {
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  BRAID_TRY(check_common(pool, pool_dtype, n_slots, H, G, SS, HD, slot_idx, B));
+  if (B == 0) return ok();
+  BRAID_TRY(check_rows(q, q_row, (int64_t)G * SS, "q"));
+  BRAID_TRY(check_rows(k, k_row, (int64_t)G * SS, "k"));
+  BRAID_TRY(check_rows(v, v_row, (int64_t)H * HD, "v"));
+  if (alpha == nullptr || beta == nullptr)
+    return fail(BRAID_EINVAL, "alpha/beta must be non-null");
+  BRAID_TRY(check_dense(y, "y"));
+  BRAID_TRY(validate_slots(slot_idx, B, n_slots, true, stream));
+  return launch_decode(pool, pool_dtype, slot_idx, B, H, G, q, q_row, k, k_row, v, v_row,
+                       PrecomputedGates{alpha, beta}, y, stream);
+}
+
+extern "C" int braid_gdn_decode_raw(void* pool, int pool_dtype, int64_t n_slots, int H, int G,
+                                    int SS, int HD, const int32_t* slot_idx, int B,
+                                    const float* q, int64_t q_row, const float* k,
+                                    int64_t k_row, const float* v, int64_t v_row,
+                                    const void* a_raw, const void* b_raw, int act_dtype,
+                                    const float* A, const float* dt_bias, float* y,
+                                    void* stream_) {
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  BRAID_TRY(check_common(pool, pool_dtype, n_slots, H, G, SS, HD, slot_idx, B));
+  BRAID_TRY(check_act(a_raw, b_raw, act_dtype, A, dt_bias));
+  if (B == 0) return ok();
+  BRAID_TRY(check_rows(q, q_row, (int64_t)G * SS, "q"));
+  BRAID_TRY(check_rows(k, k_row, (int64_t)G * SS, "k"));
+  BRAID_TRY(check_rows(v, v_row, (int64_t)H * HD, "v"));
+  BRAID_TRY(check_dense(y, "y"));
+  BRAID_TRY(validate_slots(slot_idx, B, n_slots, true, stream));
+  if (act_dtype == BRAID_F32) {
+    RawGates<F32> gates{static_cast<const float*>(a_raw), static_cast<const float*>(b_raw), A,
+                        dt_bias, nullptr};
+    return launch_decode(pool, pool_dtype, slot_idx, B, H, G, q, q_row, k, k_row, v, v_row,
+                         gates, y, stream);
+  }
+  RawGates<BF16> gates{static_cast<const uint16_t*>(a_raw), static_cast<const uint16_t*>(b_raw),
+                       A, dt_bias, nullptr};
+  return launch_decode(pool, pool_dtype, slot_idx, B, H, G, q, q_row, k, k_row, v, v_row, gates,
+                       y, stream);
+}
+
+extern "C" int braid_gdn_prefill(void* pool, int pool_dtype, int64_t n_slots, int H, int G,
+                                 int SS, int HD, const int32_t* slot_idx, int B, int T,
+                                 const float* q, const float* k, const float* v,
+                                 const float* alpha, const float* beta, float* y,
+                                 void* stream_) {
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  BRAID_TRY(check_common(pool, pool_dtype, n_slots, H, G, SS, HD, slot_idx, B));
+  if (T < 0) return fail(BRAID_EINVAL, "T must be non-negative");
+  if (B == 0) return ok();
+  if (T > 0) {
+    BRAID_TRY(check_dense(q, "q"));
+    BRAID_TRY(check_dense(k, "k"));
+    BRAID_TRY(check_dense(v, "v"));
+    BRAID_TRY(check_dense(y, "y"));
+    if (alpha == nullptr || beta == nullptr)
+      return fail(BRAID_EINVAL, "alpha/beta must be non-null");
+  }
+  BRAID_TRY(validate_slots(slot_idx, B, n_slots, true, stream));
+  return launch_prefill(pool, pool_dtype, slot_idx, B, T, H, G, q, k, v,
+                        PrecomputedGates{alpha, beta}, y, stream);
+}
+
+extern "C" int braid_gdn_prefill_raw(void* pool, int pool_dtype, int64_t n_slots, int H, int G,
+                                     int SS, int HD, const int32_t* slot_idx, int B, int T,
+                                     const float* q, const float* k, const float* v,
+                                     const void* a_raw, const void* b_raw, int act_dtype,
+                                     const float* A, const float* dt_bias, float* y,
+                                     const int32_t* seq_lens, void* stream_) {
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  BRAID_TRY(check_common(pool, pool_dtype, n_slots, H, G, SS, HD, slot_idx, B));
+  if (T < 0) return fail(BRAID_EINVAL, "T must be non-negative");
+  BRAID_TRY(check_act(a_raw, b_raw, act_dtype, A, dt_bias));
+  if (B == 0) return ok();
+  if (T > 0) {
+    BRAID_TRY(check_dense(q, "q"));
+    BRAID_TRY(check_dense(k, "k"));
+    BRAID_TRY(check_dense(v, "v"));
+    BRAID_TRY(check_dense(y, "y"));
+  }
+  BRAID_TRY(validate_slots(slot_idx, B, n_slots, true, stream));
+  if (act_dtype == BRAID_F32) {
+    RawGates<F32> gates{static_cast<const float*>(a_raw), static_cast<const float*>(b_raw), A,
+                        dt_bias, seq_lens};
+    return launch_prefill(pool, pool_dtype, slot_idx, B, T, H, G, q, k, v, gates, y, stream);
+  }
+  RawGates<BF16> gates{static_cast<const uint16_t*>(a_raw), static_cast<const uint16_t*>(b_raw),
+                       A, dt_bias, seq_lens};
+  return launch_prefill(pool, pool_dtype, slot_idx, B, T, H, G, q, k, v, gates, y, stream);
+}

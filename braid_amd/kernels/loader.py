@@ -1,0 +1,296 @@
+"""``load_gdn()``: the six GDN hot-path entry points over the C ABI.
+
+Drop-in for ``braid.kernels.loader.load_gdn`` (braid/kernels/loader.py:10-44),
+which JIT-built a pybind11 module exposing ``gdn_decode``, ``gdn_prefill``,
+``gdn_decode_raw``, ``gdn_prefill_raw``, ``conv1d_decode`` and ``quantize_act``
+(braid/kernels/csrc/bindings.cpp:25-34). Here the kernels live in the
+prebuilt gfx950 library ``braid_amd/libbraid_gdn.so`` (C ABI declared in
+``include/braid_gdn.h``) and this module is the thin torch-facing layer:
+
+* the same call signatures, argument meaning and in-place semantics;
+* the same argument checks, raising ``RuntimeError`` with the message
+  fragments the reference's tests match ("rows overlap", "out of range",
+  "duplicate ... distinct", "only SS=HD=128", ...);
+* work is enqueued on torch's current stream of the pool's device, with no
+  implicit synchronisation except the eager slot validation the library
+  performs (skipped while the stream is capturing a graph);
+* ``quantize_act`` allocates its outputs (and the small partial-max
+  workspace) in torch, as the reference's did.
+
+There is no CPU or torch fallback: if the library is missing or a tensor is
+not on the GPU, the call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+from functools import lru_cache
+from pathlib import Path
+from typing import Optional
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent.parent / "libbraid_gdn.so"
+
+BRAID_F32, BRAID_F16, BRAID_BF16 = 0, 1, 2
+_POOL_DTYPES = {torch.float32: BRAID_F32, torch.float16: BRAID_F16,
+                torch.bfloat16: BRAID_BF16}
+_ACT_DTYPES = {torch.float32: BRAID_F32, torch.bfloat16: BRAID_BF16}
+_QUANT_DTYPES = {torch.float32: BRAID_F32, torch.float16: BRAID_F16,
+                 torch.bfloat16: BRAID_BF16}
+
+_vp, _i32, _i64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
+
+# Argument lists of the exported entry points, in include/braid_gdn.h order.
+SIGNATURES = {
+    "braid_abi_version": ([], _i32),
+    "braid_last_error": ([], ctypes.c_char_p),
+    "braid_gdn_decode": ([_vp, _i32, _i64, _i32, _i32, _i32, _i32, _vp, _i32,
+                          _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp], _i32),
+    "braid_gdn_decode_raw": ([_vp, _i32, _i64, _i32, _i32, _i32, _i32, _vp, _i32,
+                              _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _i32,
+                              _vp, _vp, _vp, _vp], _i32),
+    "braid_gdn_prefill": ([_vp, _i32, _i64, _i32, _i32, _i32, _i32, _vp, _i32, _i32,
+                           _vp, _vp, _vp, _vp, _vp, _vp, _vp], _i32),
+    "braid_gdn_prefill_raw": ([_vp, _i32, _i64, _i32, _i32, _i32, _i32, _vp, _i32, _i32,
+                               _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp,
+                               _vp], _i32),
+    "braid_conv1d_decode": ([_vp, _i64, _i32, _i32, _vp, _i32, _vp, _i32, _vp, _vp,
+                             _vp, _vp], _i32),
+    "braid_quantize_act_workspace": ([_i64], _i32),
+    "braid_quantize_act": ([_vp, _i32, _i64, _vp, _vp, _vp, _vp], _i32),
+}
+
+
+def open_library(path: Path = LIB_PATH) -> ctypes.CDLL:
+    """dlopen the kernel library and declare every entry point's prototype.
+
+    torch is imported first on purpose: the library links ``libamdhip64.so.7``
+    and the dynamic linker then binds it to the HIP runtime torch already
+    loaded, so torch's streams and device pointers are valid in it.
+    """
+    if not path.exists():
+        raise RuntimeError(
+            f"{path.name} is not built at {path}; run `python -m braid_amd.build` "
+            "(the GDN kernels have no fallback)")
+    lib = ctypes.CDLL(str(path))
+    for name, (args, res) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = res
+    return lib
+
+
+def _check(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _row_stride_3d(t: torch.Tensor, name: str, require_cuda: bool = True) -> int:
+    """Batch stride of a [B, X, Y] fp32 operand whose last two dims are dense
+    (gdn_decode.cu:303-311): only the batch stride may differ, and rows may
+    not overlap."""
+    _check((t.is_cuda or not require_cuda) and t.dtype == torch.float32,
+           f"{name} must be cuda fp32")
+    _check(t.dim() == 3, f"{name} must be 3-d")
+    _check(t.stride(2) == 1 and t.stride(1) == t.size(2),
+           f"{name} must be dense in its last two dims (only the batch stride may "
+           f"differ; got strides {tuple(t.stride())})")
+    _check(t.size(0) <= 1 or t.stride(0) >= t.size(1) * t.size(2), f"{name} rows overlap")
+    return max(t.stride(0), t.size(1) * t.size(2))
+
+
+def _check_pool(pool: torch.Tensor, slot_idx: torch.Tensor) -> int:
+    _check(pool.is_cuda, "pool must be cuda")
+    _check(pool.dtype in _POOL_DTYPES, "state pool must be fp32, fp16 or bf16")
+    _check(slot_idx.dtype == torch.int32, "slot_idx must be int32")
+    _check(slot_idx.is_cuda and slot_idx.is_contiguous(), "slot_idx must be contiguous cuda")
+    _check(pool.is_contiguous(), "pool must be contiguous")
+    _check(pool.dim() == 4, "pool shape must be [S_max, H, SS, HD]")
+    return _POOL_DTYPES[pool.dtype]
+
+
+def _check_dense_f32(ts, msg: str) -> None:
+    for t in ts:
+        _check(t.is_cuda and t.dtype == torch.float32 and t.is_contiguous(), msg)
+
+
+def _check_raw(a_raw, b_raw, A, dt_bias) -> int:
+    _check(a_raw.dtype in _ACT_DTYPES,
+           "a_raw/b_raw must be fp32 or bf16 (the activation dtypes braid runs)")
+    _check(b_raw.dtype == a_raw.dtype, "a_raw and b_raw must share a dtype")
+    for t in (a_raw, b_raw):
+        _check(t.is_cuda and t.is_contiguous(), "a_raw/b_raw must be contiguous cuda")
+    _check_dense_f32((A, dt_bias), "A/dt_bias must be contiguous cuda fp32")
+    return _ACT_DTYPES[a_raw.dtype]
+
+
+class GDNKernels:
+    """The loaded module: one method per reference entry point."""
+
+    def __init__(self, lib: ctypes.CDLL):
+        self._lib = lib
+        self.abi_version = lib.braid_abi_version()
+
+    # -- plumbing -------------------------------------------------------------
+
+    def _call(self, fn_name: str, device: torch.device, *args) -> None:
+        with torch.cuda.device(device):
+            stream = torch.cuda.current_stream(device).cuda_stream
+            rc = getattr(self._lib, fn_name)(*args, stream)
+        if rc != 0:
+            raise RuntimeError(self._lib.braid_last_error().decode())
+
+    # -- GDN scans ------------------------------------------------------------
+
+    def gdn_decode(self, pool, slot_idx, q, k, v, alpha, beta, y) -> None:
+        """One token for B rows; pool updated in place at slot_idx rows
+        (gdn_decode.cu:313-360)."""
+        pdt = _check_pool(pool, slot_idx)
+        _check_dense_f32((alpha, beta, y), "alpha/beta/y must be contiguous cuda fp32")
+        q_row, k_row, v_row = (_row_stride_3d(q, "q"), _row_stride_3d(k, "k"),
+                               _row_stride_3d(v, "v"))
+        B, G, SS = q.shape
+        H, HD = v.size(1), v.size(2)
+        self._check_decode_shapes(pool, slot_idx, q, k, v, y, B, G, SS, H, HD)
+        _check(alpha.numel() == B * H and beta.numel() == B * H, "alpha/beta must be [B, H]")
+        self._call("braid_gdn_decode", pool.device, _ptr(pool), pdt, pool.size(0), H, G, SS,
+                   HD, _ptr(slot_idx), B, _ptr(q), q_row, _ptr(k), k_row, _ptr(v), v_row,
+                   _ptr(alpha), _ptr(beta), _ptr(y))
+
+    def gdn_decode_raw(self, pool, slot_idx, q, k, v, a_raw, b_raw, A, dt_bias, y) -> None:
+        """Decode with alpha/beta computed in-kernel from the raw projections
+        (gdn_decode.cu:367-441)."""
+        pdt = _check_pool(pool, slot_idx)
+        _check(y.is_cuda and y.dtype == torch.float32 and y.is_contiguous(),
+               "y must be contiguous cuda fp32")
+        q_row, k_row, v_row = (_row_stride_3d(q, "q"), _row_stride_3d(k, "k"),
+                               _row_stride_3d(v, "v"))
+        adt = _check_raw(a_raw, b_raw, A, dt_bias)
+        B, G, SS = q.shape
+        H, HD = v.size(1), v.size(2)
+        self._check_decode_shapes(pool, slot_idx, q, k, v, y, B, G, SS, H, HD)
+        _check(a_raw.dim() >= 1 and a_raw.size(0) == B and a_raw.numel() == B * H,
+               "a_raw must be [B, H]")
+        _check(b_raw.shape == a_raw.shape, "b_raw must match a_raw")
+        _check(A.numel() == H and dt_bias.numel() == H, "A and dt_bias must be [H]")
+        self._call("braid_gdn_decode_raw", pool.device, _ptr(pool), pdt, pool.size(0), H, G,
+                   SS, HD, _ptr(slot_idx), B, _ptr(q), q_row, _ptr(k), k_row, _ptr(v), v_row,
+                   _ptr(a_raw), _ptr(b_raw), adt, _ptr(A), _ptr(dt_bias), _ptr(y))
+
+    @staticmethod
+    def _check_decode_shapes(pool, slot_idx, q, k, v, y, B, G, SS, H, HD) -> None:
+        _check(SS == 128 and HD == 128, "only SS=HD=128 is instantiated")
+        _check(H % G == 0, "n_heads must be divisible by n_groups")
+        _check(k.shape == q.shape, "k must match q")
+        _check(v.size(0) == B, "v must match q in B")
+        _check(slot_idx.numel() == B, "slot_idx must have one entry per batch row")
+        _check(tuple(pool.shape[1:]) == (H, SS, HD), "pool shape must be [S_max, H, SS, HD]")
+        _check(tuple(y.shape) == (B, H, HD), "y shape must be [B, H, HD]")
+
+    def gdn_prefill(self, pool, slot_idx, q, k, v, alpha, beta, y) -> None:
+        """T tokens per launch, state on chip between them
+        (gdn_decode.cu:553-603). Caller pads with alpha=1, beta=0."""
+        pdt = _check_pool(pool, slot_idx)
+        _check_dense_f32((q, k, v, alpha, beta, y), "all operands must be contiguous cuda fp32")
+        B, T, G, SS, H, HD = self._check_prefill_shapes(pool, slot_idx, q, k, v, y)
+        _check(tuple(alpha.shape) == (B, T, H), "alpha must be [B, T, H]")
+        _check(beta.shape == alpha.shape, "beta must match alpha")
+        self._call("braid_gdn_prefill", pool.device, _ptr(pool), pdt, pool.size(0), H, G, SS,
+                   HD, _ptr(slot_idx), B, T, _ptr(q), _ptr(k), _ptr(v), _ptr(alpha),
+                   _ptr(beta), _ptr(y))
+
+    def gdn_prefill_raw(self, pool, slot_idx, q, k, v, a_raw, b_raw, A, dt_bias, y,
+                        seq_lens: Optional[torch.Tensor] = None) -> None:
+        """Chunk scan with in-kernel gates and ragged seq_lens
+        (gdn_decode.cu:611-699). seq_lens=None means every column is live."""
+        pdt = _check_pool(pool, slot_idx)
+        _check_dense_f32((q, k, v, y), "q/k/v/y must be contiguous cuda fp32")
+        adt = _check_raw(a_raw, b_raw, A, dt_bias)
+        B, T, G, SS, H, HD = self._check_prefill_shapes(pool, slot_idx, q, k, v, y)
+        _check(a_raw.dim() >= 2 and a_raw.size(0) == B and a_raw.size(1) == T
+               and a_raw.numel() == B * T * H, "a_raw must be [B, T, H]")
+        _check(b_raw.shape == a_raw.shape, "b_raw must match a_raw")
+        _check(A.numel() == H and dt_bias.numel() == H, "A and dt_bias must be [H]")
+        if seq_lens is not None:
+            _check(seq_lens.is_cuda and seq_lens.dtype == torch.int32
+                   and seq_lens.is_contiguous(), "seq_lens must be contiguous cuda int32")
+            _check(seq_lens.numel() == B, "seq_lens must have one entry per batch row")
+        self._call("braid_gdn_prefill_raw", pool.device, _ptr(pool), pdt, pool.size(0), H, G,
+                   SS, HD, _ptr(slot_idx), B, T, _ptr(q), _ptr(k), _ptr(v), _ptr(a_raw),
+                   _ptr(b_raw), adt, _ptr(A), _ptr(dt_bias), _ptr(y), _ptr(seq_lens))
+
+    @staticmethod
+    def _check_prefill_shapes(pool, slot_idx, q, k, v, y):
+        _check(q.dim() == 4 and v.dim() == 4, "q/k must be [B, T, G, SS], v [B, T, H, HD]")
+        B, T, G, SS = q.shape
+        H, HD = v.size(2), v.size(3)
+        _check(SS == 128 and HD == 128, "only SS=HD=128 is instantiated")
+        _check(H % G == 0, "n_heads must be divisible by n_groups")
+        _check(slot_idx.numel() == B, "slot_idx must have one entry per batch row")
+        _check(k.shape == q.shape, "k must match q")
+        _check(v.size(0) == B and v.size(1) == T, "v must match q in [B, T]")
+        _check(tuple(pool.shape[1:]) == (H, SS, HD), "pool shape must be [S_max, H, SS, HD]")
+        _check(tuple(y.shape) == (B, T, H, HD), "y shape must be [B, T, H, HD]")
+        return B, T, G, SS, H, HD
+
+    # -- conv -----------------------------------------------------------------
+
+    def conv1d_decode(self, conv_pool, slot_idx, x, weight, bias, out) -> None:
+        """Slotted causal conv1d decode step + SiLU (conv1d_decode.cu:91-149).
+        `bias` may be None or empty."""
+        _check(conv_pool.is_cuda and conv_pool.dtype == torch.float32,
+               "conv_pool must be cuda fp32")
+        _check(conv_pool.is_contiguous(), "conv_pool must be contiguous")
+        _check(slot_idx.dtype == torch.int32, "slot_idx must be int32")
+        _check(slot_idx.is_cuda and slot_idx.is_contiguous(), "slot_idx must be contiguous cuda")
+        _check(conv_pool.dim() == 3, "conv_pool must be [S_max, C, K]")
+        n_slots, C, K = conv_pool.shape
+        B = x.size(0)
+        _check(K <= 8, "conv_kernel > 8 is not instantiated")
+        _check(x.dim() == 2 and x.size(1) == C and tuple(out.shape) == (B, C),
+               "x/out must be [B, C]")
+        _check(tuple(weight.shape) == (C, K), "weight must be [C, K]")
+        _check_dense_f32((weight,), "weight must be contiguous cuda fp32")
+        _check(slot_idx.numel() == B, "slot_idx must have one entry per batch row")
+        _check(x.dtype in _ACT_DTYPES,
+               "x must be fp32 or bf16 (the activation dtypes braid runs)")
+        _check(x.is_cuda and x.is_contiguous(), "x must be contiguous")
+        _check(out.is_cuda and out.dtype == torch.float32 and out.is_contiguous(),
+               "out must be contiguous fp32")
+        bias_p = None
+        if bias is not None and bias.numel() > 0:
+            _check_dense_f32((bias,), "bias must be contiguous cuda fp32")
+            _check(bias.numel() == C, "bias must be [C]")
+            bias_p = _ptr(bias)
+        self._call("braid_conv1d_decode", conv_pool.device, _ptr(conv_pool), n_slots, C, K,
+                   _ptr(slot_idx), B, _ptr(x), _ACT_DTYPES[x.dtype], _ptr(weight), bias_p,
+                   _ptr(out))
+
+    # -- FP8 activation quant ---------------------------------------------------
+
+    def quantize_act(self, x: torch.Tensor) -> list:
+        """x -> [q (float8_e4m3fn, x's shape), scale ([1, 1] fp32)]
+        (quant_act.cu:140-176)."""
+        _check(x.is_cuda, "x must be cuda")
+        _check(x.is_contiguous(), "x must be contiguous")
+        _check(x.dtype in _QUANT_DTYPES, "activation must be fp32, bf16 or fp16")
+        n = x.numel()
+        _check(n > 0, "x must not be empty")
+        q = torch.empty(x.shape, dtype=torch.float8_e4m3fn, device=x.device)
+        scale = torch.empty((1, 1), dtype=torch.float32, device=x.device)
+        partial = torch.empty(self._lib.braid_quantize_act_workspace(n), dtype=torch.float32,
+                              device=x.device)
+        self._call("braid_quantize_act", x.device, _ptr(x), _QUANT_DTYPES[x.dtype], n,
+                   _ptr(q), _ptr(scale), _ptr(partial))
+        return [q, scale]
+
+
+@lru_cache(maxsize=1)
+def load_gdn() -> GDNKernels:
+    """Load the prebuilt gfx950 kernel library (no JIT; build with
+    ``python -m braid_amd.build``)."""
+    return GDNKernels(open_library())

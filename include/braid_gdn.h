@@ -1,0 +1,160 @@
+/*
+ * braid_gdn.h — C ABI of the MI355X (gfx950) Gated DeltaNet mixer hot path.
+ *
+ * One shared library, libbraid_gdn.so, exports these entry points. They take
+ * plain device pointers, element counts/strides and a hipStream_t (passed as
+ * void* so this header needs no HIP include), enqueue work on that stream and
+ * return 0 on success. On failure they return a nonzero braid_status and
+ * braid_last_error() returns a thread-local, human-readable message. Nothing
+ * here allocates device memory; every output buffer and workspace belongs to
+ * the caller.
+ *
+ * Each entry replaces one function of the reference's pybind11 module
+ * (braid/kernels/csrc/bindings.cpp:25-34); the citation on each declaration
+ * names the reference function whose behaviour it reproduces.
+ *
+ * Slot validation: every state-pool entry point checks the device slot map
+ * (range and, for the GDN scans, distinctness) by copying it to the host —
+ * unless the stream is capturing a graph, where a device->host copy would be
+ * illegal. This mirrors braid/kernels/csrc/gdn_decode.cu:280-297 and
+ * conv1d_decode.cu:77-89.
+ */
+#ifndef BRAID_GDN_H
+#define BRAID_GDN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types of the state pool, the activations and the conv input. */
+enum braid_dtype {
+  BRAID_F32 = 0,
+  BRAID_F16 = 1,
+  BRAID_BF16 = 2,
+};
+
+enum braid_status {
+  BRAID_OK = 0,
+  BRAID_EINVAL = 1,    /* bad argument: shape, dtype, null pointer, overlap */
+  BRAID_ESLOT = 2,     /* slot map out of range or (GDN scans) not distinct */
+  BRAID_EHIP = 3,      /* a HIP runtime call failed */
+};
+
+/* ABI version; bumped on any signature change. */
+int braid_abi_version(void);
+
+/* Message for the last failing call on this thread ("" when none). */
+const char* braid_last_error(void);
+
+/*
+ * Batched GDN decode step, precomputed gates.
+ * Replaces gdn_decode (braid/kernels/csrc/gdn_decode.cu:313-360).
+ *
+ *   pool     [n_slots, H, SS, HD] of pool_dtype, updated in place at the rows
+ *            named by slot_idx only
+ *   slot_idx [B] int32, device
+ *   q, k     [B, G, SS] fp32; the last two dims dense, batch row stride
+ *            q_row / k_row elements (>= G*SS)
+ *   v        [B, H, HD] fp32, batch row stride v_row (>= H*HD)
+ *   alpha, beta [B, H] fp32 dense
+ *   y        [B, H, HD] fp32 dense, written
+ * SS and HD must be 128; H % G == 0.
+ */
+int braid_gdn_decode(void* pool, int pool_dtype, int64_t n_slots, int H, int G,
+                     int SS, int HD, const int32_t* slot_idx, int B,
+                     const float* q, int64_t q_row, const float* k,
+                     int64_t k_row, const float* v, int64_t v_row,
+                     const float* alpha, const float* beta, float* y,
+                     void* stream);
+
+/*
+ * Batched GDN decode step with the gates computed in-kernel from the raw
+ * projections. Replaces gdn_decode_raw (gdn_decode.cu:367-441).
+ *
+ *   a_raw, b_raw [B, H] of act_dtype (BRAID_F32 or BRAID_BF16), dense
+ *   A, dt_bias   [H] fp32 (A already -exp(A_log))
+ *   beta  = widen(round_act(1 / (1 + exp(-b))))
+ *   alpha = exp(A * softplus(a + dt_bias)), softplus(x) = x > 20 ? x : log1p(exp(x))
+ */
+int braid_gdn_decode_raw(void* pool, int pool_dtype, int64_t n_slots, int H,
+                         int G, int SS, int HD, const int32_t* slot_idx, int B,
+                         const float* q, int64_t q_row, const float* k,
+                         int64_t k_row, const float* v, int64_t v_row,
+                         const void* a_raw, const void* b_raw, int act_dtype,
+                         const float* A, const float* dt_bias, float* y,
+                         void* stream);
+
+/*
+ * Chunk prefill scan: T tokens per launch, state held on chip between them.
+ * Replaces gdn_prefill (gdn_decode.cu:553-603).
+ *
+ *   q, k [B, T, G, SS], v and y [B, T, H, HD], alpha/beta [B, T, H]; all fp32
+ *   dense. The caller pads with alpha = 1, beta = 0 (an exact identity step).
+ * The result equals braid_gdn_decode applied T times, bit for bit, for every
+ * pool dtype (the on-chip state is kept in the pool's storage type).
+ */
+int braid_gdn_prefill(void* pool, int pool_dtype, int64_t n_slots, int H,
+                      int G, int SS, int HD, const int32_t* slot_idx, int B,
+                      int T, const float* q, const float* k, const float* v,
+                      const float* alpha, const float* beta, float* y,
+                      void* stream);
+
+/*
+ * Chunk prefill scan with in-kernel gates and ragged lengths.
+ * Replaces gdn_prefill_raw (gdn_decode.cu:611-699).
+ *
+ *   a_raw, b_raw [B, T, H] of act_dtype, dense
+ *   seq_lens     [B] int32 device, or NULL (every column live). A column
+ *                t >= seq_lens[b] runs alpha = 1, beta = 0. 0 and values > T
+ *                are legal.
+ */
+int braid_gdn_prefill_raw(void* pool, int pool_dtype, int64_t n_slots, int H,
+                          int G, int SS, int HD, const int32_t* slot_idx,
+                          int B, int T, const float* q, const float* k,
+                          const float* v, const void* a_raw, const void* b_raw,
+                          int act_dtype, const float* A, const float* dt_bias,
+                          float* y, const int32_t* seq_lens, void* stream);
+
+/*
+ * Batched slotted causal depthwise conv1d, one decode step, SiLU fused.
+ * Replaces conv1d_decode (braid/kernels/csrc/conv1d_decode.cu:91-149).
+ *
+ *   conv_pool [n_slots, C, K] fp32, window of the last K pre-conv inputs,
+ *             oldest first, K contiguous per channel; updated in place
+ *   x         [B, C] of x_dtype (BRAID_F32 or BRAID_BF16), dense
+ *   weight    [C, K] fp32; bias [C] fp32 or NULL
+ *   out       [B, C] fp32: SiLU(sum_i window[i] * weight[c, i] + bias[c])
+ * K must be 2, 3, 4 or 8. Slots are range-checked only (no distinctness).
+ */
+int braid_conv1d_decode(float* conv_pool, int64_t n_slots, int C, int K,
+                        const int32_t* slot_idx, int B, const void* x,
+                        int x_dtype, const float* weight, const float* bias,
+                        float* out, void* stream);
+
+/*
+ * Number of fp32 partials braid_quantize_act needs as workspace for an
+ * n-element activation.
+ */
+int braid_quantize_act_workspace(int64_t n);
+
+/*
+ * Dynamic per-tensor FP8 e4m3fn activation quantization, two launches.
+ * Replaces quantize_act (braid/kernels/csrc/quant_act.cu:140-176), which
+ * allocated its outputs; here the caller passes them.
+ *
+ *   x       n contiguous elements of x_dtype (F32, F16 or BF16), n > 0
+ *   q       n bytes, e4m3fn codes
+ *   scale   1 fp32: max(amax(|x|) * fl(1/448), 1e-12), NaN if x holds NaN
+ *   partial braid_quantize_act_workspace(n) fp32 scratch
+ * q = e4m3fn(clamp(x / scale, -448, 448)), round to nearest even.
+ */
+int braid_quantize_act(const void* x, int x_dtype, int64_t n, uint8_t* q,
+                       float* scale, float* partial, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BRAID_GDN_H */

@@ -1,0 +1,99 @@
+"""Input builders and comparison helpers shared by the GPU parity tests."""
+from __future__ import annotations
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+import oracle
+
+DEV = "cuda"
+KIND = {torch.float32: "f32", torch.float16: "f16", torch.bfloat16: "bf16"}
+
+# Kernel-vs-oracle tolerance for fp32 arithmetic (the reference's own gate,
+# tests/test_gdn_decode_kernel.py:36-37).
+RTOL, ATOL = 2e-5, 2e-6
+
+
+def gen(seed: int) -> torch.Generator:
+    return torch.Generator(device=DEV).manual_seed(seed)
+
+
+def decode_inputs(B, H=8, G=4, seed=0):
+    g = gen(seed)
+    return dict(
+        q=torch.randn(B, G, 128, generator=g, device=DEV),
+        k=torch.randn(B, G, 128, generator=g, device=DEV),
+        v=torch.randn(B, H, 128, generator=g, device=DEV),
+        alpha=torch.rand(B, H, generator=g, device=DEV) * 0.5 + 0.5,
+        beta=torch.rand(B, H, generator=g, device=DEV),
+    )
+
+
+def prefill_inputs(B, T, H=8, G=4, seed=3):
+    g = gen(seed)
+    return dict(
+        q=torch.randn(B, T, G, 128, generator=g, device=DEV),
+        k=torch.randn(B, T, G, 128, generator=g, device=DEV),
+        v=torch.randn(B, T, H, 128, generator=g, device=DEV),
+        alpha=torch.rand(B, T, H, generator=g, device=DEV),
+        beta=torch.rand(B, T, H, generator=g, device=DEV),
+    )
+
+
+def raw_gates(shape, H, dt, seed=7):
+    """a_raw/b_raw of `shape` in the activation dtype plus A (= -exp(A_log)) and
+    dt_bias, as the reference's tests draw them (test_gdn_raw_gates.py:72-83)."""
+    g = gen(seed)
+    a_raw = (torch.randn(*shape, generator=g, device=DEV) * 2).to(dt).contiguous()
+    b_raw = (torch.randn(*shape, generator=g, device=DEV) * 2).to(dt).contiguous()
+    A = -torch.exp(torch.randn(H, generator=g, device=DEV) * 0.5)
+    dt_bias = torch.randn(H, generator=g, device=DEV) * 0.5
+    return a_raw, b_raw, A.contiguous(), dt_bias.contiguous()
+
+
+def torch_gates(a_raw, b_raw, A, dt_bias):
+    """braid/model/gdn.py:299-300 exactly: sigmoid in the activation dtype then
+    widened; alpha fp32 throughout. The in-kernel gates must equal this to the bit."""
+    beta = torch.sigmoid(b_raw).float()
+    alpha = torch.exp(A * F.softplus(a_raw.float() + dt_bias))
+    return alpha.contiguous(), beta.contiguous()
+
+
+def pool(S, H=8, dtype=torch.float32, seed=11, scale=0.1):
+    p = torch.randn(S, H, 128, 128, generator=gen(seed), device=DEV) * scale
+    return p.to(dtype).contiguous()
+
+
+def to_np_pool(p: torch.Tensor) -> np.ndarray:
+    """A device pool as the oracle's storage array."""
+    if p.dtype == torch.bfloat16:
+        return p.view(torch.uint16).cpu().numpy().copy()
+    return p.cpu().numpy().copy()
+
+
+def act_np(t: torch.Tensor) -> np.ndarray:
+    """Activation tensor for the oracle: fp32 values, or bf16 bit patterns."""
+    if t.dtype == torch.bfloat16:
+        return t.view(torch.uint16).cpu().numpy()
+    return t.float().cpu().numpy()
+
+
+def ulp16(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """Distance in units in the last place between two arrays of 16-bit floats
+    (fp16 arrays, or bf16 bit patterns as uint16)."""
+    def ordered(x):
+        u = np.asarray(x).view(np.uint16).astype(np.int64)
+        return np.where(u & 0x8000, 0x8000 - u, u)
+    return np.abs(ordered(a) - ordered(b))
+
+
+def assert_pool_close(kern_pool: torch.Tensor, ref: np.ndarray, rows, what=""):
+    """fp32 pools within the fp32 tolerance; 16-bit pools within one ulp."""
+    got = to_np_pool(kern_pool)[rows]
+    exp = ref[rows]
+    if kern_pool.dtype == torch.float32:
+        np.testing.assert_allclose(got, exp, rtol=RTOL, atol=ATOL, err_msg=what)
+    else:
+        d = ulp16(got, exp)
+        assert d.max() <= 1, f"{what}: {int((d > 1).sum())} elements beyond 1 ulp (max {d.max()})"

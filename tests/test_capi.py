@@ -1,0 +1,130 @@
+"""The C-ABI library on the CPU: it loads, exports every symbol the header
+declares, and rejects bad arguments before touching a GPU.
+
+No compute call is made here (there is no GPU in the build container); the
+error paths exercised return before any HIP call.
+"""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from braid_amd.kernels import loader
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "braid_gdn.h"
+
+
+def _declared() -> list[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(braid_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not loader.LIB_PATH.exists():
+        from braid_amd.build import build
+        build()
+    return loader.open_library()
+
+
+def test_header_declares_the_six_reference_entry_points():
+    names = _declared()
+    for fn in ("braid_gdn_decode", "braid_gdn_decode_raw", "braid_gdn_prefill",
+               "braid_gdn_prefill_raw", "braid_conv1d_decode", "braid_quantize_act"):
+        assert fn in names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in _declared():
+        assert hasattr(lib, name), f"{name} declared in {HEADER.name} but not exported"
+    assert set(_declared()) == set(loader.SIGNATURES), "ctypes prototypes out of sync with header"
+    assert lib.braid_abi_version() == 1
+
+
+def _err(lib) -> str:
+    return lib.braid_last_error().decode()
+
+
+def test_decode_rejects_bad_shapes_before_any_gpu_call(lib):
+    fake = ctypes.c_void_p(4096)  # never dereferenced: every case fails host-side
+    rc = lib.braid_gdn_decode(fake, 1, 160, 32, 16, 64, 128, fake, 4, fake, 2048, fake, 2048,
+                              fake, 4096, fake, fake, fake, None)
+    assert rc == 1 and "only SS=HD=128" in _err(lib)
+    rc = lib.braid_gdn_decode(fake, 7, 160, 32, 16, 128, 128, fake, 4, fake, 2048, fake, 2048,
+                              fake, 4096, fake, fake, fake, None)
+    assert rc == 1 and "fp32, fp16 or bf16" in _err(lib)
+    rc = lib.braid_gdn_decode(fake, 1, 160, 32, 12, 128, 128, fake, 4, fake, 2048, fake, 2048,
+                              fake, 4096, fake, fake, fake, None)
+    assert rc == 1 and "divisible" in _err(lib)
+    rc = lib.braid_gdn_decode(fake, 1, 160, 32, 16, 128, 128, fake, 4, fake, 1000, fake, 2048,
+                              fake, 4096, fake, fake, fake, None)
+    assert rc == 1 and "rows overlap" in _err(lib)
+
+
+def test_zero_batch_is_a_no_op(lib):
+    fake = ctypes.c_void_p(4096)
+    rc = lib.braid_gdn_decode(fake, 1, 160, 32, 16, 128, 128, fake, 0, None, 0, None, 0,
+                              None, 0, None, None, None, None)
+    assert rc == 0 and _err(lib) == ""
+
+
+def test_raw_and_conv_and_quant_reject_bad_arguments(lib):
+    fake = ctypes.c_void_p(4096)
+    rc = lib.braid_gdn_decode_raw(fake, 1, 8, 4, 2, 128, 128, fake, 2, fake, 256, fake, 256,
+                                  fake, 512, fake, fake, 1, fake, fake, fake, None)
+    assert rc == 1 and "fp32 or bf16" in _err(lib)
+    rc = lib.braid_conv1d_decode(fake, 8, 512, 5, fake, 2, fake, 0, fake, None, fake, None)
+    assert rc == 1 and "not instantiated" in _err(lib)
+    rc = lib.braid_conv1d_decode(fake, 8, 512, 4, fake, 2, fake, 1, fake, None, fake, None)
+    assert rc == 1 and "fp32 or bf16" in _err(lib)
+    rc = lib.braid_quantize_act(fake, 2, 0, fake, fake, fake, None)
+    assert rc == 1 and "empty" in _err(lib)
+    rc = lib.braid_quantize_act(fake, 9, 16, fake, fake, fake, None)
+    assert rc == 1 and "fp32, bf16 or fp16" in _err(lib)
+    assert lib.braid_quantize_act_workspace(64 * 4096) == 128
+    assert lib.braid_quantize_act_workspace(10 ** 9) == 1024
+
+
+def test_prefill_rejects_negative_t(lib):
+    fake = ctypes.c_void_p(4096)
+    rc = lib.braid_gdn_prefill(fake, 0, 8, 4, 2, 128, 128, fake, 2, -1, fake, fake, fake,
+                               fake, fake, fake, None)
+    assert rc == 1 and "non-negative" in _err(lib)
+
+
+# --- the torch-facing shim: checks that fire before the library is called -----
+
+def _shim():
+    return loader.GDNKernels.__new__(loader.GDNKernels)
+
+
+def test_shim_refuses_cpu_tensors_and_bad_dtypes():
+    k = _shim()
+    pool = torch.zeros(4, 2, 128, 128)
+    slots = torch.zeros(1, dtype=torch.int32)
+    q = torch.zeros(1, 1, 128)
+    with pytest.raises(RuntimeError, match="pool must be cuda"):
+        k.gdn_decode(pool, slots, q, q, torch.zeros(1, 2, 128), torch.zeros(1, 2),
+                     torch.zeros(1, 2), torch.zeros(1, 2, 128))
+    with pytest.raises(RuntimeError, match="x must be cuda"):
+        k.quantize_act(torch.zeros(4, 4))
+    with pytest.raises(RuntimeError, match="conv_pool must be cuda fp32"):
+        k.conv1d_decode(torch.zeros(2, 8, 4), slots, torch.zeros(1, 8), torch.zeros(8, 4),
+                        None, torch.zeros(1, 8))
+
+
+def test_row_stride_rules_match_the_reference():
+    buf = torch.zeros(3, 8192)
+    q = buf[:, :2048].unflatten(-1, (16, 128))
+    assert loader._row_stride_3d(q, "q", require_cuda=False) == 8192
+    with pytest.raises(RuntimeError, match="rows overlap"):
+        loader._row_stride_3d(torch.zeros(4, 2, 128).as_strided((4, 2, 128), (128, 128, 1)), "q",
+                              require_cuda=False)
+    with pytest.raises(RuntimeError, match="dense in its last two dims"):
+        loader._row_stride_3d(torch.zeros(2, 128, 2).transpose(1, 2), "q", require_cuda=False)

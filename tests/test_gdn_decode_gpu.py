@@ -1,0 +1,263 @@
+"""gdn_decode / gdn_decode_raw on the GPU, through the C ABI, against the oracle.
+
+Mirrors the reference's kernel gates (tests/test_gdn_decode_kernel.py,
+test_slot_indirection.py, test_gdn_raw_gates.py:106-202, test_copy_kill.py:97-162)
+with the CPU oracle as the checker instead of the reference's torch oracle.
+"""
+from __future__ import annotations
+
+import time
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from gpu_helpers import (ATOL, DEV, KIND, RTOL, act_np, assert_pool_close, decode_inputs, gen,
+                         pool, raw_gates, to_np_pool, torch_gates)
+
+pytestmark = pytest.mark.gpu
+GOLDEN = Path(__file__).resolve().parent / "golden"
+POOL_DTYPES = [torch.float32, torch.float16, torch.bfloat16]
+POOL_IDS = ["f32-pool", "f16-pool", "bf16-pool"]
+
+
+def _np(d):
+    return {k: v.cpu().numpy() for k, v in d.items()}
+
+
+@pytest.mark.parametrize("B", [1, 2, 8, 32])
+def test_decode_matches_oracle(kern, B):
+    p = pool(64)
+    slots = torch.arange(B, dtype=torch.int32, device=DEV)
+    inp = decode_inputs(B)
+    ref_pool = to_np_pool(p)
+    n = _np(inp)
+    y_ref = oracle.gdn_decode(ref_pool, np.arange(B), n["q"], n["k"], n["v"], n["alpha"],
+                              n["beta"], "f32")
+    y = torch.empty(B, 8, 128, device=DEV)
+    kern.gdn_decode(p, slots, inp["q"], inp["k"], inp["v"], inp["alpha"], inp["beta"], y)
+    np.testing.assert_allclose(y.cpu().numpy(), y_ref, rtol=RTOL, atol=ATOL)
+    assert_pool_close(p, ref_pool, slice(0, 64))
+
+
+@pytest.mark.parametrize("dt", POOL_DTYPES, ids=POOL_IDS)
+def test_decode_each_pool_dtype_matches_oracle(kern, dt):
+    B = 8
+    p = pool(20, dtype=dt, seed=5)
+    slots = torch.tensor([19, 0, 7, 3, 12, 5, 11, 2], dtype=torch.int32, device=DEV)
+    inp = decode_inputs(B, seed=6)
+    ref_pool = to_np_pool(p)
+    n = _np(inp)
+    y_ref = oracle.gdn_decode(ref_pool, slots.cpu().numpy(), n["q"], n["k"], n["v"], n["alpha"],
+                              n["beta"], KIND[dt])
+    y = torch.empty(B, 8, 128, device=DEV)
+    kern.gdn_decode(p, slots, inp["q"], inp["k"], inp["v"], inp["alpha"], inp["beta"], y)
+    np.testing.assert_allclose(y.cpu().numpy(), y_ref, rtol=RTOL, atol=ATOL)
+    assert_pool_close(p, ref_pool, slice(0, 20), f"{dt} pool")
+
+
+def test_decode_matches_golden_float64_fixture(kern):
+    g = np.load(GOLDEN / "decode_f64.npz")
+    p = torch.from_numpy(g["state"]).to(DEV).contiguous()
+    t = {k: torch.from_numpy(g[k]).to(DEV).contiguous() for k in ("q", "k", "v", "alpha", "beta")}
+    y = torch.empty(1, 2, 128, device=DEV)
+    kern.gdn_decode(p, torch.zeros(1, dtype=torch.int32, device=DEV), t["q"], t["k"], t["v"],
+                    t["alpha"], t["beta"], y)
+    np.testing.assert_allclose(y.cpu().numpy(), g["y"], rtol=RTOL, atol=ATOL)
+    np.testing.assert_allclose(p.cpu().numpy(), g["state_out"], rtol=RTOL, atol=ATOL)
+
+
+def test_nonidentity_slots_are_honoured_and_others_untouched(kern):
+    p = pool(16, H=4)
+    untouched = p.clone()
+    slots = torch.tensor([7, 3], dtype=torch.int32, device=DEV)
+    inp = decode_inputs(2, H=4, G=2)
+    ref_pool = to_np_pool(p)
+    n = _np(inp)
+    y_ref = oracle.gdn_decode(ref_pool, [7, 3], n["q"], n["k"], n["v"], n["alpha"], n["beta"],
+                              "f32")
+    y = torch.empty(2, 4, 128, device=DEV)
+    kern.gdn_decode(p, slots, inp["q"], inp["k"], inp["v"], inp["alpha"], inp["beta"], y)
+    np.testing.assert_allclose(y.cpu().numpy(), y_ref, rtol=RTOL, atol=ATOL)
+    assert_pool_close(p, ref_pool, [7, 3])
+    for s in (0, 1, 2, 4, 5, 6, 8, 15):
+        assert torch.equal(p[s], untouched[s])
+
+
+def test_rows_do_not_leak_into_each_other(kern):
+    pa = pool(8)
+    pb = pa.clone()
+    two = decode_inputs(2, seed=11)
+    y2 = torch.empty(2, 8, 128, device=DEV)
+    kern.gdn_decode(pa, torch.tensor([0, 1], dtype=torch.int32, device=DEV), two["q"], two["k"],
+                    two["v"], two["alpha"], two["beta"], y2)
+    solo = {k: v[1:2].contiguous() for k, v in two.items()}
+    y1 = torch.empty(1, 8, 128, device=DEV)
+    kern.gdn_decode(pb, torch.tensor([1], dtype=torch.int32, device=DEV), solo["q"], solo["k"],
+                    solo["v"], solo["alpha"], solo["beta"], y1)
+    assert torch.equal(y2[1:2], y1)
+    assert torch.equal(pa[1], pb[1])
+
+
+def test_repeated_slot_is_rejected(kern):
+    p = pool(8, H=4)
+    inp = decode_inputs(2, H=4, G=2)
+    y = torch.empty(2, 4, 128, device=DEV)
+    with pytest.raises(RuntimeError, match="duplicate|distinct"):
+        kern.gdn_decode(p, torch.tensor([2, 2], dtype=torch.int32, device=DEV), inp["q"],
+                        inp["k"], inp["v"], inp["alpha"], inp["beta"], y)
+
+
+def test_out_of_range_slot_is_rejected(kern):
+    p = pool(8, H=4)
+    inp = decode_inputs(2, H=4, G=2)
+    y = torch.empty(2, 4, 128, device=DEV)
+    for bad in ([0, 99], [-1, 0]):
+        with pytest.raises(RuntimeError, match="range|bounds"):
+            kern.gdn_decode(p, torch.tensor(bad, dtype=torch.int32, device=DEV), inp["q"],
+                            inp["k"], inp["v"], inp["alpha"], inp["beta"], y)
+
+
+def _strided_qkv(B, H=32, G=16, seed=7):
+    """q/k/v as column slices of one [B, C] conv-output buffer (row stride C)."""
+    C = 2 * G * 128 + H * 128
+    buf = torch.randn(B, C, generator=gen(seed), device=DEV)
+    q, k, v = torch.split(buf, [G * 128, G * 128, H * 128], dim=-1)
+    return (q.unflatten(-1, (G, 128)), k.unflatten(-1, (G, 128)), v.unflatten(-1, (H, 128)))
+
+
+@pytest.mark.parametrize("B", [1, 5])
+def test_strided_qkv_equals_contiguous(kern, B):
+    q, k, v = _strided_qkv(B)
+    if B > 1:
+        assert not q.is_contiguous()
+    alpha = torch.rand(B, 32, generator=gen(9), device=DEV)
+    beta = torch.rand(B, 32, generator=gen(10), device=DEV)
+    slots = torch.arange(B, dtype=torch.int32, device=DEV)
+    p1, p2 = pool(B, H=32), pool(B, H=32)
+    y1, y2 = torch.empty(B, 32, 128, device=DEV), torch.empty(B, 32, 128, device=DEV)
+    kern.gdn_decode(p1, slots, q.contiguous(), k.contiguous(), v.contiguous(), alpha, beta, y1)
+    kern.gdn_decode(p2, slots, q, k, v, alpha, beta, y2)
+    assert torch.equal(y1, y2) and torch.equal(p1, p2)
+    a_raw, b_raw, A, dtb = raw_gates((B, 32), 32, torch.bfloat16, seed=23)
+    kern.gdn_decode_raw(p1, slots, q.contiguous(), k.contiguous(), v.contiguous(), a_raw, b_raw,
+                        A, dtb, y1)
+    kern.gdn_decode_raw(p2, slots, q, k, v, a_raw, b_raw, A, dtb, y2)
+    assert torch.equal(y1, y2) and torch.equal(p1, p2)
+
+
+@pytest.mark.parametrize("pool_dt", POOL_DTYPES, ids=POOL_IDS)
+@pytest.mark.parametrize("act", [torch.float32, torch.bfloat16], ids=["f32-act", "bf16-act"])
+@pytest.mark.parametrize("B", [1, 5])
+def test_raw_gates_equal_the_torch_computed_ones_bitwise(kern, B, act, pool_dt):
+    inp = decode_inputs(B, H=32, G=16, seed=3)
+    a_raw, b_raw, A, dtb = raw_gates((B, 32), 32, act)
+    alpha, beta = torch_gates(a_raw, b_raw, A, dtb)
+    slots = torch.arange(B, dtype=torch.int32, device=DEV)
+    p1, p2 = pool(B, H=32, dtype=pool_dt), pool(B, H=32, dtype=pool_dt)
+    y1, y2 = torch.empty(B, 32, 128, device=DEV), torch.empty(B, 32, 128, device=DEV)
+    kern.gdn_decode(p1, slots, inp["q"], inp["k"], inp["v"], alpha, beta, y1)
+    kern.gdn_decode_raw(p2, slots, inp["q"], inp["k"], inp["v"], a_raw, b_raw, A, dtb, y2)
+    assert torch.equal(y1, y2), f"outputs differ by {(y1 - y2).abs().max().item():.3e}"
+    assert torch.equal(p1, p2), "states differ"
+
+
+def test_raw_gates_match_the_oracle_gates(kern):
+    """The in-kernel gates against the oracle's gate restatement (tolerance:
+    the device and host transcendentals are different implementations)."""
+    B, H = 4, 32
+    inp = decode_inputs(B, H=H, G=16, seed=13)
+    a_raw, b_raw, A, dtb = raw_gates((B, H), H, torch.bfloat16, seed=14)
+    ref_pool = to_np_pool(pool(B, H=H))
+    p = pool(B, H=H)
+    al, be = oracle.gdn_gates(act_np(a_raw), act_np(b_raw), A.cpu().numpy(),
+                              dtb.cpu().numpy(), "bf16")
+    n = _np(inp)
+    y_ref = oracle.gdn_decode(ref_pool, np.arange(B), n["q"], n["k"], n["v"], al, be, "f32")
+    y = torch.empty(B, H, 128, device=DEV)
+    kern.gdn_decode_raw(p, torch.arange(B, dtype=torch.int32, device=DEV), inp["q"], inp["k"],
+                        inp["v"], a_raw, b_raw, A, dtb, y)
+    np.testing.assert_allclose(y.cpu().numpy(), y_ref, rtol=1e-4, atol=1e-5)
+    np.testing.assert_allclose(p.cpu().numpy(), ref_pool, rtol=1e-4, atol=1e-5)
+
+
+def test_softplus_threshold_branch_matches_torch(kern):
+    B, H = 1, 32
+    inp = decode_inputs(B, H=H, G=16, seed=21)
+    _, b_raw, A, _ = raw_gates((B, H), H, torch.float32, seed=23)
+    dtb = torch.zeros(H, device=DEV)
+    a_raw = torch.zeros(B, H, device=DEV)
+    probes = [-80.0, -20.0, 0.0, 19.0, 19.999999, 20.0, 20.000001, 25.0, 80.0]
+    a_raw[0, : len(probes)] = torch.tensor(probes, device=DEV)
+    alpha, beta = torch_gates(a_raw, b_raw, A, dtb)
+    slots = torch.zeros(1, dtype=torch.int32, device=DEV)
+    p1, p2 = pool(1, H=H), pool(1, H=H)
+    y1, y2 = torch.empty(1, H, 128, device=DEV), torch.empty(1, H, 128, device=DEV)
+    kern.gdn_decode(p1, slots, inp["q"], inp["k"], inp["v"], alpha, beta, y1)
+    kern.gdn_decode_raw(p2, slots, inp["q"], inp["k"], inp["v"], a_raw, b_raw, A, dtb, y2)
+    assert torch.equal(y1, y2) and torch.equal(p1, p2), "gates differ across the threshold"
+
+
+def _capture(kern, fn):
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            fn()
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fn()
+    return graph
+
+
+def test_graph_replay_survives_slot_reassignment(kern):
+    B, H = 4, 8
+    p = torch.zeros(32, H, 128, 128, device=DEV)
+    slots = torch.arange(B, dtype=torch.int32, device=DEV)
+    q = torch.zeros(B, 4, 128, device=DEV)
+    k = torch.zeros(B, 4, 128, device=DEV)
+    v = torch.zeros(B, H, 128, device=DEV)
+    alpha = torch.zeros(B, H, device=DEV)
+    beta = torch.zeros(B, H, device=DEV)
+    y = torch.zeros(B, H, 128, device=DEV)
+    graph = _capture(kern, lambda: kern.gdn_decode(p, slots, q, k, v, alpha, beta, y))
+    g = gen(7)
+    for assignment in ([5, 9, 1, 30], [0, 1, 2, 3], [31, 2, 17, 8]):
+        p.normal_(generator=g)
+        q.normal_(generator=g)
+        k.normal_(generator=g)
+        v.normal_(generator=g)
+        alpha.uniform_(0.5, 1.0, generator=g)
+        beta.uniform_(0.0, 1.0, generator=g)
+        slots.copy_(torch.tensor(assignment, dtype=torch.int32, device=DEV))
+        ref_pool = to_np_pool(p)
+        y_ref = oracle.gdn_decode(ref_pool, assignment, q.cpu().numpy(), k.cpu().numpy(),
+                                  v.cpu().numpy(), alpha.cpu().numpy(), beta.cpu().numpy(), "f32")
+        graph.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_allclose(y.cpu().numpy(), y_ref, rtol=RTOL, atol=ATOL)
+        assert_pool_close(p, ref_pool, slice(0, 32))
+
+
+def test_replay_with_rotating_slots_is_cheap(kern):
+    B, H = 8, 32
+    p = pool(32, H=H)
+    slots = torch.arange(B, dtype=torch.int32, device=DEV)
+    inp = decode_inputs(B, H=H, G=16)
+    y = torch.empty(B, H, 128, device=DEV)
+    graph = _capture(kern, lambda: kern.gdn_decode(p, slots, inp["q"], inp["k"], inp["v"],
+                                                   inp["alpha"], inp["beta"], y))
+    rotations = [torch.tensor([(i + r) % 32 for i in range(B)], dtype=torch.int32, device=DEV)
+                 for r in range(8)]
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    for r in range(200):
+        slots.copy_(rotations[r % 8])
+        graph.replay()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t) / 200 * 1e3
+    print(f"\n  rotating replay {ms:.4f} ms/step")
+    assert ms < 1.0

@@ -1,0 +1,187 @@
+"""gdn_prefill / gdn_prefill_raw on the GPU, through the C ABI.
+
+Mirrors the reference's chunk-scan gates (tests/test_gdn_prefill_kernel.py:84-206,
+test_gdn_raw_gates.py:150-256): the chunk equals the decode kernel applied T
+times bit for bit — here for fp32, fp16 AND bf16 pools, because the chunk
+keeps its on-chip state in the pool's storage type — a pad column is an exact
+identity, chunking is invisible, and raw gates / seq_lens equal the torch
+spelling bit for bit. Plus parity with the oracle.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from gpu_helpers import (ATOL, DEV, KIND, RTOL, assert_pool_close, pool, prefill_inputs,
+                         raw_gates, to_np_pool, torch_gates)
+
+pytestmark = pytest.mark.gpu
+POOL_DTYPES = [torch.float32, torch.float16, torch.bfloat16]
+POOL_IDS = ["f32-pool", "f16-pool", "bf16-pool"]
+
+
+def _decode_t_times(kern, p, slots, q, k, v, alpha, beta):
+    B, T = q.shape[:2]
+    H = v.size(2)
+    y = torch.empty(B, T, H, 128, device=DEV)
+    for t in range(T):
+        out = torch.empty(B, H, 128, device=DEV)
+        kern.gdn_decode(p, slots, q[:, t].contiguous(), k[:, t].contiguous(),
+                        v[:, t].contiguous(), alpha[:, t].contiguous(), beta[:, t].contiguous(),
+                        out)
+        y[:, t] = out
+    return y
+
+
+@pytest.mark.parametrize("T", [1, 4, 17, 128])
+@pytest.mark.parametrize("B", [1, 5])
+def test_chunk_equals_decode_applied_t_times(kern, T, B):
+    inp = prefill_inputs(B, T, H=32, G=16)
+    slots = torch.arange(B, dtype=torch.int32, device=DEV)
+    pc = pool(B, H=32)
+    yc = torch.empty(B, T, 32, 128, device=DEV)
+    kern.gdn_prefill(pc, slots, inp["q"], inp["k"], inp["v"], inp["alpha"], inp["beta"], yc)
+    ps = pool(B, H=32)
+    ys = _decode_t_times(kern, ps, slots, **inp)
+    assert torch.equal(yc, ys), f"outputs differ by {(yc - ys).abs().max().item():.3e}"
+    assert torch.equal(pc, ps), f"states differ by {(pc - ps).abs().max().item():.3e}"
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16], ids=["f16-pool", "bf16-pool"])
+def test_a_narrow_pool_chunk_is_bit_identical_to_decode(kern, dt):
+    """Stronger than the reference (which allowed 8 eps here): the chunk rounds
+    its on-chip state through the pool type after every token, as T decode
+    launches do, so the two are the same computation."""
+    B, T = 3, 24
+    inp = prefill_inputs(B, T, seed=9)
+    slots = torch.tensor([4, 0, 2], dtype=torch.int32, device=DEV)
+    pc = pool(6, dtype=dt)
+    yc = torch.empty(B, T, 8, 128, device=DEV)
+    kern.gdn_prefill(pc, slots, inp["q"], inp["k"], inp["v"], inp["alpha"], inp["beta"], yc)
+    ps = pool(6, dtype=dt)
+    ys = _decode_t_times(kern, ps, slots, **inp)
+    assert torch.equal(yc, ys) and torch.equal(pc, ps)
+
+
+@pytest.mark.parametrize("dt", POOL_DTYPES, ids=POOL_IDS)
+def test_chunk_matches_oracle(kern, dt):
+    B, T = 3, 17
+    inp = prefill_inputs(B, T, seed=12)
+    slots = torch.tensor([5, 1, 3], dtype=torch.int32, device=DEV)
+    p = pool(6, dtype=dt, seed=13)
+    ref_pool = to_np_pool(p)
+    n = {k: v.cpu().numpy() for k, v in inp.items()}
+    y_ref = oracle.gdn_prefill(ref_pool, [5, 1, 3], n["q"], n["k"], n["v"], n["alpha"],
+                               n["beta"], KIND[dt])
+    y = torch.empty(B, T, 8, 128, device=DEV)
+    kern.gdn_prefill(p, slots, inp["q"], inp["k"], inp["v"], inp["alpha"], inp["beta"], y)
+    # errors stay at one rounding per token: the update is non-expansive
+    # (alpha <= 1, I - beta k k^T with |k| = 1 and beta in [0, 1])
+    np.testing.assert_allclose(y.cpu().numpy(), y_ref, rtol=1e-4, atol=1e-5)
+    if dt == torch.float32:
+        np.testing.assert_allclose(p.cpu().numpy(), ref_pool, rtol=1e-4, atol=1e-5)
+    else:
+        from gpu_helpers import ulp16
+        d = ulp16(to_np_pool(p), ref_pool)
+        assert d.max() <= 2 and (d <= 1).mean() > 0.9999, f"max {d.max()} ulp"
+
+
+def test_a_pad_column_does_not_move_the_state(kern):
+    B, T = 4, 6
+    inp = prefill_inputs(B, T, seed=21)
+    slots = torch.arange(B, dtype=torch.int32, device=DEV)
+    lens = torch.tensor([2, 3, 4, 6], device=DEV)
+    live = (torch.arange(T, device=DEV)[None] < lens[:, None])[:, :, None]
+    am = torch.where(live, inp["alpha"], 1.0).contiguous()
+    bm = torch.where(live, inp["beta"], 0.0).contiguous()
+    padded = pool(B)
+    y = torch.empty(B, T, 8, 128, device=DEV)
+    kern.gdn_prefill(padded, slots, inp["q"], inp["k"], inp["v"], am, bm, y)
+    for b in range(B):
+        n = int(lens[b])
+        solo = pool(B)[b:b + 1].contiguous()
+        y1 = torch.empty(1, n, 8, 128, device=DEV)
+        kern.gdn_prefill(solo, torch.zeros(1, dtype=torch.int32, device=DEV),
+                         inp["q"][b:b + 1, :n].contiguous(), inp["k"][b:b + 1, :n].contiguous(),
+                         inp["v"][b:b + 1, :n].contiguous(), am[b:b + 1, :n].contiguous(),
+                         bm[b:b + 1, :n].contiguous(), y1)
+        assert torch.equal(padded[b], solo[0]), f"row {b} state moved under padding"
+        assert torch.equal(y[b, :n], y1[0]), f"row {b} outputs moved"
+
+
+@pytest.mark.parametrize("cut", [1, 7, 64])
+def test_two_chunks_leave_the_same_state_as_one(kern, cut):
+    B, T = 2, 96
+    inp = prefill_inputs(B, T, seed=33)
+    slots = torch.arange(B, dtype=torch.int32, device=DEV)
+    whole = pool(B)
+    yw = torch.empty(B, T, 8, 128, device=DEV)
+    kern.gdn_prefill(whole, slots, inp["q"], inp["k"], inp["v"], inp["alpha"], inp["beta"], yw)
+    parts = pool(B)
+    yp = torch.empty(B, T, 8, 128, device=DEV)
+    for lo, hi in ((0, cut), (cut, T)):
+        out = torch.empty(B, hi - lo, 8, 128, device=DEV)
+        kern.gdn_prefill(parts, slots, *(inp[n][:, lo:hi].contiguous()
+                                         for n in ("q", "k", "v", "alpha", "beta")), out)
+        yp[:, lo:hi] = out
+    assert torch.equal(whole, parts) and torch.equal(yw, yp)
+
+
+@pytest.mark.parametrize("act", [torch.float32, torch.bfloat16], ids=["f32-act", "bf16-act"])
+@pytest.mark.parametrize("T", [1, 17, 96])
+def test_prefill_raw_gates_equal_the_torch_computed_ones(kern, T, act):
+    B = 3
+    inp = prefill_inputs(B, T, H=32, G=16, seed=31)
+    a_raw, b_raw, A, dtb = raw_gates((B, T, 32), 32, act, seed=33)
+    alpha, beta = torch_gates(a_raw, b_raw, A, dtb)
+    slots = torch.arange(B, dtype=torch.int32, device=DEV)
+    p1, p2 = pool(B, H=32), pool(B, H=32)
+    y1, y2 = torch.empty(B, T, 32, 128, device=DEV), torch.empty(B, T, 32, 128, device=DEV)
+    kern.gdn_prefill(p1, slots, inp["q"], inp["k"], inp["v"], alpha, beta, y1)
+    kern.gdn_prefill_raw(p2, slots, inp["q"], inp["k"], inp["v"], a_raw, b_raw, A, dtb, y2, None)
+    assert torch.equal(y1, y2) and torch.equal(p1, p2)
+
+
+def test_seq_lens_is_the_where_mask_bit_for_bit(kern):
+    B, T = 4, 12
+    inp = prefill_inputs(B, T, H=32, G=16, seed=41)
+    a_raw, b_raw, A, dtb = raw_gates((B, T, 32), 32, torch.bfloat16, seed=43)
+    alpha, beta = torch_gates(a_raw, b_raw, A, dtb)
+    lens = torch.tensor([3, 7, 12, 1], device=DEV, dtype=torch.int32)
+    live = (torch.arange(T, device=DEV)[None] < lens[:, None])[:, :, None]
+    am = torch.where(live, alpha, 1.0).contiguous()
+    bm = torch.where(live, beta, 0.0).contiguous()
+    slots = torch.arange(B, dtype=torch.int32, device=DEV)
+    p1, p2 = pool(B, H=32), pool(B, H=32)
+    y1, y2 = torch.empty(B, T, 32, 128, device=DEV), torch.empty(B, T, 32, 128, device=DEV)
+    kern.gdn_prefill(p1, slots, inp["q"], inp["k"], inp["v"], am, bm, y1)
+    kern.gdn_prefill_raw(p2, slots, inp["q"], inp["k"], inp["v"], a_raw, b_raw, A, dtb, y2, lens)
+    assert torch.equal(p1, p2) and torch.equal(y1, y2)
+
+
+def test_a_len_of_zero_and_a_len_beyond_t_are_legal(kern):
+    B, T = 2, 6
+    inp = prefill_inputs(B, T, H=32, G=16, seed=51)
+    a_raw, b_raw, A, dtb = raw_gates((B, T, 32), 32, torch.float32, seed=53)
+    slots = torch.arange(B, dtype=torch.int32, device=DEV)
+    lens = torch.tensor([0, T + 5], device=DEV, dtype=torch.int32)
+    p = pool(B, H=32)
+    before = p[0].clone()
+    y = torch.empty(B, T, 32, 128, device=DEV)
+    kern.gdn_prefill_raw(p, slots, inp["q"], inp["k"], inp["v"], a_raw, b_raw, A, dtb, y, lens)
+    assert torch.equal(p[0], before)
+    pr = pool(B, H=32)
+    yr = torch.empty_like(y)
+    kern.gdn_prefill_raw(pr, slots, inp["q"], inp["k"], inp["v"], a_raw, b_raw, A, dtb, yr, None)
+    assert torch.equal(p[1], pr[1]) and torch.equal(y[1], yr[1])
+
+
+def test_prefill_rejects_duplicate_slots(kern):
+    inp = prefill_inputs(2, 3)
+    p = pool(4)
+    y = torch.empty(2, 3, 8, 128, device=DEV)
+    with pytest.raises(RuntimeError, match="duplicate|distinct"):
+        kern.gdn_prefill(p, torch.tensor([1, 1], dtype=torch.int32, device=DEV), inp["q"],
+                         inp["k"], inp["v"], inp["alpha"], inp["beta"], y)
