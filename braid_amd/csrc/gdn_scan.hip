@@ -1,7 +1,7 @@
 // Batched Gated DeltaNet decode step and chunk prefill scan for gfx950.
 //
-// Both kernels launch one 256-thread workgroup (four waves, one per 32-column
-// panel) per (batch row, value head) tile and run the same per-token device
+// Both kernels launch one 256-thread workgroup (four waves, 32 state rows
+// each) per (batch row, value head) tile and run the same per-token device
 // function, braid::gdn_token. Decode loads the tile from the slot-indexed pool,
 // runs one token and stores it back; prefill loads it once, runs T tokens with
 // the tile resident in registers (in the pool's storage type) and stores it
@@ -37,13 +37,14 @@ gdn_decode_kernel(typename Storage<Tag>::T* __restrict__ pool,
 
   // The slot comes from device memory, so one captured graph serves any slot
   // assignment (gdn_decode.cu:230-236).
+  __shared__ TileLds lds;
   const int slot = slot_idx[b];
   ST* tile = pool + ((size_t)slot * H + h) * (kSS * kHD) + L.col0;
 
   // Issue the whole tile's loads first; the norms and gates below overlap them.
   Row8<Tag> S[kRowsPerLane];
 #pragma unroll
-  for (int i = 0; i < kRowsPerLane; ++i) S[i].load(tile + (size_t)L.row(i) * kHD);
+  for (int i = 0; i < kRowsPerLane; ++i) S[i].load_nt(tile + (size_t)L.row(i) * kHD);
 
   float vv[8];
   load8(v + (size_t)b * v_row + (size_t)h * kHD + L.col0, vv);
@@ -54,11 +55,12 @@ gdn_decode_kernel(typename Storage<Tag>::T* __restrict__ pool,
   gates.get(b, h, 0, H, 1, a, bt);
 
   float yy[8];
-  gdn_token<Tag>(S, qk, vv, a, bt, yy);
+  gdn_token<Tag>(L, S, qk, vv, a, bt, lds, yy);
 
 #pragma unroll
-  for (int i = 0; i < kRowsPerLane; ++i) S[i].store(tile + (size_t)L.row(i) * kHD);
-  if (L.rg == 0) store8(y + ((size_t)b * H + h) * kHD + L.col0, yy);
+  for (int i = 0; i < kRowsPerLane; ++i) S[i].store_nt(tile + (size_t)L.row(i) * kHD);
+  // Each column chunk's totals sit in all 16 of its lanes; wave w writes chunks 4w..4w+3.
+  if (L.rg == 0 && (L.c8 >> 2) == L.wave) store8(y + ((size_t)b * H + h) * kHD + L.col0, yy);
 }
 
 template <class Tag, class Gates>
@@ -74,12 +76,13 @@ gdn_prefill_kernel(typename Storage<Tag>::T* __restrict__ pool,
   const int g = h / heads_per_group;
   const LaneMap L(threadIdx.x);
 
+  __shared__ TileLds lds;
   const int slot = slot_idx[b];
   ST* tile = pool + ((size_t)slot * H + h) * (kSS * kHD) + L.col0;
 
   Row8<Tag> S[kRowsPerLane];
 #pragma unroll
-  for (int i = 0; i < kRowsPerLane; ++i) S[i].load(tile + (size_t)L.row(i) * kHD);
+  for (int i = 0; i < kRowsPerLane; ++i) S[i].load_nt(tile + (size_t)L.row(i) * kHD);
 
   for (int t = 0; t < T; ++t) {
     const size_t bt_idx = (size_t)b * T + t;
@@ -90,12 +93,12 @@ gdn_prefill_kernel(typename Storage<Tag>::T* __restrict__ pool,
     float a, bt;
     gates.get(b, h, t, H, T, a, bt);
     float yy[8];
-    gdn_token<Tag>(S, qk, vv, a, bt, yy);
-    if (L.rg == 0) store8(y + (bt_idx * H + h) * kHD + L.col0, yy);
+    gdn_token<Tag>(L, S, qk, vv, a, bt, lds, yy);
+    if (L.rg == 0 && (L.c8 >> 2) == L.wave) store8(y + (bt_idx * H + h) * kHD + L.col0, yy);
   }
 
 #pragma unroll
-  for (int i = 0; i < kRowsPerLane; ++i) S[i].store(tile + (size_t)L.row(i) * kHD);
+  for (int i = 0; i < kRowsPerLane; ++i) S[i].store_nt(tile + (size_t)L.row(i) * kHD);
 }
 
 // ---------------------------------------------------------------------------

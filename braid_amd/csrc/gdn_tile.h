@@ -1,20 +1,26 @@
-// Per-wave Gated DeltaNet tile step for gfx950 (CDNA4, wave64).
+// Gated DeltaNet tile step for gfx950 (CDNA4, wave64).
 //
 // One (sequence slot, value head) state tile is S[s, d], s = key index (rows,
 // SS = 128), d = value index (columns, HD = 128), row-major with d contiguous:
-// the pool layout [n_slots, H, SS, HD] of braid/model/cache.py:127-128.
+// the pool layout [n_slots, H, SS, HD] of braid/model/cache.py:127-128. A row
+// is 256 bytes of an fp16 pool.
 //
-// The tile is cut into four 32-column PANELS and each panel belongs to one
-// wave. Every reduction of the recurrence runs over rows s for a fixed column
-// d, so a panel carries everything its columns need: the four waves of a tile
-// never exchange data, never touch LDS and never wait on a barrier.
+// A tile belongs to one 256-thread workgroup: wave w owns the 32 full rows
+// [32w, 32w + 32). Lane l of a wave owns the 8-column chunk c8 = l % 16 of rows
+// 32w + r + 4i (r = l / 16, i = 0..7), so each of a lane's eight state accesses
+// is one 16-byte vector and every wave-wide load or store instruction covers
+// four consecutive rows — 1 KiB contiguous for fp16. Measured on MI355X, this
+// whole-row pattern streams ~10% faster than per-wave column panels, and the
+// state goes through nontemporal loads and stores (it is touched once per
+// step and never re-read by the step).
 //
-// Inside a wave, lane l owns an 8-column chunk (cq = l % 4) of rows
-// rg + 16 * i (rg = l / 4, i = 0..7): eight 16-byte row pieces of an fp16 pool,
-// loaded and stored as 128-bit accesses. The sums over s are taken in a fixed
-// order — sequentially over the lane's eight rows, then a butterfly over the
-// sixteen row groups — which makes every lane of a column hold bit-identical
-// totals and makes the result a pure function of the inputs.
+// Every reduction of the recurrence runs over rows s for a fixed column d, in
+// one fixed order that defines the result's bits:
+//   1. sequentially over a lane's eight rows (an fma chain, i = 0..7);
+//   2. a butterfly over the four row groups r of a wave (lane xor 16, then xor
+//      32): partners add the same two operands, so all lanes agree bitwise;
+//   3. across the four waves through LDS, summed as (w0 + w1) + (w2 + w3) by
+//      every lane that needs the total.
 //
 // The state lives in registers in its STORAGE type. Each token widens it to
 // fp32, runs the recurrence in fp32 and narrows it back, exactly as a decode
@@ -38,21 +44,22 @@
 
 namespace braid {
 
-constexpr int kSS = 128;                       // key dim (state rows)
-constexpr int kHD = 128;                       // value dim (state columns)
-constexpr int kPanel = 32;                     // columns per wave
-constexpr int kLanesPerRow = kPanel / 8;       // 8 columns per lane
-constexpr int kRowGroups = 64 / kLanesPerRow;  // 16
-constexpr int kRowsPerLane = kSS / kRowGroups; // 8
-constexpr int kWavesPerTile = kHD / kPanel;    // 4
-constexpr int kTileThreads = 64 * kWavesPerTile;
+constexpr int kSS = 128;                          // key dim (state rows)
+constexpr int kHD = 128;                          // value dim (state columns)
+constexpr int kWaves = 4;                         // waves per tile
+constexpr int kRowsPerWave = kSS / kWaves;        // 32
+constexpr int kChunks = kHD / 8;                  // 16 eight-column chunks per row
+constexpr int kRowGroups = 64 / kChunks;          // 4 row groups per wave
+constexpr int kRowsPerLane = kRowsPerWave / kRowGroups;  // 8
+constexpr int kTileThreads = 64 * kWaves;
 constexpr float kL2Eps = 1e-6f;
 // 128^-0.5 correctly rounded to fp32 (0x3DB504F3).
 constexpr float kYScale = 0.088388347648318440550f;
 
 // ---------------------------------------------------------------------------
 // Storage types. A Row8 is the eight consecutive elements of one state row a
-// lane owns, held in the pool's own encoding.
+// lane owns, held in the pool's own encoding. load_nt / store_nt are the
+// streaming (nontemporal) accesses used for the state.
 
 struct F32 {};
 struct F16 {};
@@ -70,7 +77,15 @@ __device__ __forceinline__ uint32_t bf16_bits_rne(float f) {
 __device__ __forceinline__ float bf16_widen(uint32_t bits16) {
   return __uint_as_float(bits16 << 16);
 }
+// fp32 -> fp16 bits, round to nearest even, of the ALREADY ROUNDED fp32 value.
+// The empty asm pins `f` in a register: without it the compiler may fuse
+// fptrunc(fma(a, b, c)) into one mixed-precision fma that rounds straight to
+// fp16 (a single rounding instead of fp32-then-fp16). That is a different
+// result in rare ties, and the compiler makes the choice per call site, so
+// decode and prefill could disagree. The reference narrows the fp32 value
+// (gdn_decode.cu:29-30); so does this.
 __device__ __forceinline__ uint32_t f16_bits_rne(float f) {
+  asm volatile("" : "+v"(f));
   return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f);
 }
 __device__ __forceinline__ float f16_widen(uint32_t bits16) {
@@ -84,13 +99,13 @@ template <>
 struct Row8<F32> {
   using elem = float;
   f32x4 lo, hi;
-  __device__ __forceinline__ void load(const float* p) {
-    lo = *reinterpret_cast<const f32x4*>(p);
-    hi = *reinterpret_cast<const f32x4*>(p + 4);
+  __device__ __forceinline__ void load_nt(const float* p) {
+    lo = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+    hi = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p + 4));
   }
-  __device__ __forceinline__ void store(float* p) const {
-    *reinterpret_cast<f32x4*>(p) = lo;
-    *reinterpret_cast<f32x4*>(p + 4) = hi;
+  __device__ __forceinline__ void store_nt(float* p) const {
+    __builtin_nontemporal_store(lo, reinterpret_cast<f32x4*>(p));
+    __builtin_nontemporal_store(hi, reinterpret_cast<f32x4*>(p + 4));
   }
   __device__ __forceinline__ float get(int c) const { return c < 4 ? lo[c] : hi[c - 4]; }
   __device__ __forceinline__ void set(int c, float x) {
@@ -102,11 +117,11 @@ template <class Tag>
 struct Row8Half {
   using elem = uint16_t;
   u32x4 raw;  // element c sits in bits 16*(c&1) of raw[c>>1]
-  __device__ __forceinline__ void load(const uint16_t* p) {
-    raw = *reinterpret_cast<const u32x4*>(p);
+  __device__ __forceinline__ void load_nt(const uint16_t* p) {
+    raw = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
   }
-  __device__ __forceinline__ void store(uint16_t* p) const {
-    *reinterpret_cast<u32x4*>(p) = raw;
+  __device__ __forceinline__ void store_nt(uint16_t* p) const {
+    __builtin_nontemporal_store(raw, reinterpret_cast<u32x4*>(p));
   }
   __device__ __forceinline__ uint32_t bits(int c) const {
     return (raw[c >> 1] >> (16 * (c & 1))) & 0xffffu;
@@ -145,10 +160,10 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-// Sum over the 16 row groups sharing a column chunk (lane bits 2..5).
+// Sum over a wave's four row groups sharing a column chunk (lane bits 4, 5).
 __device__ __forceinline__ float rowgroup_sum(float v) {
-#pragma unroll
-  for (int m = kLanesPerRow; m < 64; m <<= 1) v += xor_shuffle(v, m);
+  v += xor_shuffle(v, 16);
+  v += xor_shuffle(v, 32);
   return v;
 }
 
@@ -217,16 +232,29 @@ struct RawGates {
 // ---------------------------------------------------------------------------
 // Lane geometry within a tile.
 struct LaneMap {
+  int wave;  // 0..3: rows [32 wave, 32 wave + 32)
   int lane;  // 0..63
-  int rg;    // row group 0..15: rows rg + 16 i
-  int col0;  // first of this lane's eight columns, 0..120
+  int rg;    // row group 0..3
+  int c8;    // column chunk 0..15
+  int col0;  // first of this lane's eight columns
   __device__ __forceinline__ LaneMap(int tid) {
     lane = tid & 63;
-    const int wave = tid >> 6;
-    rg = lane / kLanesPerRow;
-    col0 = wave * kPanel + (lane % kLanesPerRow) * 8;
+    wave = tid >> 6;
+    rg = lane / kChunks;
+    c8 = lane % kChunks;
+    col0 = c8 * 8;
   }
-  __device__ __forceinline__ int row(int i) const { return rg + kRowGroups * i; }
+  __device__ __forceinline__ int row(int i) const {
+    return wave * kRowsPerWave + rg + kRowGroups * i;
+  }
+};
+
+// Cross-wave exchange buffers for one tile: per-wave column partials of kv and
+// of y, kept apart so one token's y exchange never overwrites kv partials a
+// slower wave is still reading (and vice versa across tokens).
+struct TileLds {
+  float kv[kWaves][kHD];
+  float y[kWaves][kHD];
 };
 
 // q_hat / k_hat for this lane's rows, from the dense [SS] fp32 key-group
@@ -258,13 +286,48 @@ __device__ __forceinline__ void normalize_qk(const LaneMap& L, const float* __re
   }
 }
 
-// One token of the recurrence on this lane's 8 x 8 block. `v` holds the lane's
-// eight value entries; `y` receives its eight outputs (identical in all sixteen
-// row groups).
+// Completes a column sum: the lane's chain value `part` for columns
+// col0..col0+7 is reduced over the wave's row groups, exchanged through `buf`
+// and summed over the four waves in the fixed order (w0 + w1) + (w2 + w3).
+// Every lane returns the eight column totals of its chunk.
+__device__ __forceinline__ void tile_column_sums(const LaneMap& L, float (&part)[8],
+                                                 float (*buf)[kHD]) {
+#pragma unroll
+  for (int c = 0; c < 8; ++c) part[c] = rowgroup_sum(part[c]);
+  if (L.rg == 0) {
+    f32x4 lo, hi;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      lo[c] = part[c];
+      hi[c] = part[c + 4];
+    }
+    *reinterpret_cast<f32x4*>(&buf[L.wave][L.col0]) = lo;
+    *reinterpret_cast<f32x4*>(&buf[L.wave][L.col0 + 4]) = hi;
+  }
+  __syncthreads();
+  float w[kWaves][8];
+#pragma unroll
+  for (int j = 0; j < kWaves; ++j) {
+    const f32x4 lo = *reinterpret_cast<const f32x4*>(&buf[j][L.col0]);
+    const f32x4 hi = *reinterpret_cast<const f32x4*>(&buf[j][L.col0 + 4]);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      w[j][c] = lo[c];
+      w[j][c + 4] = hi[c];
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < 8; ++c) part[c] = (w[0][c] + w[1][c]) + (w[2][c] + w[3][c]);
+}
+
+// One token of the recurrence on this lane's 8 x 8 block. `v` holds the eight
+// value entries of the lane's columns; `y` receives their outputs (identical
+// in every lane of a column chunk). Contains two workgroup barriers, so all
+// four waves of the tile must call it together.
 template <class Tag>
-__device__ __forceinline__ void gdn_token(Row8<Tag> (&S)[kRowsPerLane], const QK& qk,
-                                          const float (&v)[8], float alpha, float beta,
-                                          float (&y)[8]) {
+__device__ __forceinline__ void gdn_token(const LaneMap& L, Row8<Tag> (&S)[kRowsPerLane],
+                                          const QK& qk, const float (&v)[8], float alpha,
+                                          float beta, TileLds& lds, float (&y)[8]) {
   float kv[8];
 #pragma unroll
   for (int c = 0; c < 8; ++c) kv[c] = S[0].get(c) * qk.kh[0];
@@ -273,12 +336,11 @@ __device__ __forceinline__ void gdn_token(Row8<Tag> (&S)[kRowsPerLane], const QK
 #pragma unroll
     for (int c = 0; c < 8; ++c) kv[c] = fmaf(S[i].get(c), qk.kh[i], kv[c]);
   }
+  tile_column_sums(L, kv, lds.kv);
   float delta[8];
 #pragma unroll
-  for (int c = 0; c < 8; ++c) {
-    const float kvt = rowgroup_sum(kv[c]);
-    delta[c] = (v[c] - alpha * kvt) * beta;
-  }
+  for (int c = 0; c < 8; ++c) delta[c] = (v[c] - alpha * kv[c]) * beta;
+
   float acc[8];
 #pragma unroll
   for (int c = 0; c < 8; ++c) acc[c] = 0.f;
@@ -291,8 +353,9 @@ __device__ __forceinline__ void gdn_token(Row8<Tag> (&S)[kRowsPerLane], const QK
       acc[c] = fmaf(nv, qk.qh[i], acc[c]);
     }
   }
+  tile_column_sums(L, acc, lds.y);
 #pragma unroll
-  for (int c = 0; c < 8; ++c) y[c] = rowgroup_sum(acc[c]) * kYScale;
+  for (int c = 0; c < 8; ++c) y[c] = acc[c] * kYScale;
 }
 
 __device__ __forceinline__ void load8(const float* __restrict__ p, float (&out)[8]) {

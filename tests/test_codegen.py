@@ -1,0 +1,66 @@
+"""Properties of the gfx950 code the kernels compile to (CPU only: hipcc
+cross-compiles). These guard numerics and safety properties that a test on
+the GPU would only catch by chance:
+
+* no fp16-result mixed-precision fma (v_fma_mixlo/hi_f16): the state must be
+  narrowed from its rounded fp32 value, as the reference's StateIO does; a
+  fused single rounding differs in rare ties and the compiler picks it per
+  call site, which broke decode == prefill bit-identity for fp16 pools;
+* no packed-fp32 VALU ops (v_pk_add/mul/fma_f32), which the build disables;
+* no scalar-memory stores or atomics.
+"""
+from __future__ import annotations
+
+import re
+import shutil
+import subprocess
+
+import pytest
+
+from braid_amd import build as B
+
+SOURCES = ["gdn_scan.hip", "conv1d_decode.hip", "quant_act.hip"]
+
+
+@pytest.fixture(scope="module")
+def asm(tmp_path_factory):
+    hipcc = B.hipcc()
+    if not shutil.which(hipcc) and not __import__("os").path.exists(hipcc):
+        pytest.skip("hipcc not available")
+    out = {}
+    d = tmp_path_factory.mktemp("asm")
+    for src in SOURCES:
+        s = d / (src + ".s")
+        cmd = [hipcc, *B.common_flags(), "-x", "hip", "--cuda-device-only", "-S",
+               str(B.CSRC / src), "-o", str(s)]
+        subprocess.run(cmd, check=True, capture_output=True)
+        out[src] = s.read_text()
+    return out
+
+
+def _instructions(text):
+    return [ln.split()[0] for ln in text.splitlines()
+            if ln.strip() and ln.startswith((" ", "\t")) and not ln.strip().startswith((".", ";"))]
+
+
+@pytest.mark.parametrize("src", SOURCES)
+def test_no_fused_fp16_narrowing(asm, src):
+    assert not re.search(r"v_(fma|mad)_mix(lo|hi)_f16", asm[src])
+
+
+@pytest.mark.parametrize("src", SOURCES)
+def test_no_packed_fp32_ops(asm, src):
+    assert not re.search(r"\bv_pk_(add|mul|fma)_f32\b", asm[src])
+
+
+@pytest.mark.parametrize("src", SOURCES)
+def test_no_scalar_memory_writes(asm, src):
+    ops = set(_instructions(asm[src]))
+    bad = sorted(o for o in ops if re.match(r"s_(store|buffer_store|atomic|buffer_atomic|dcache_wb|dcache_discard)", o))
+    assert not bad, bad
+
+
+def test_decode_state_uses_128_bit_nontemporal_accesses(asm):
+    text = asm["gdn_scan.hip"]
+    assert re.search(r"global_load_dwordx4 .* nt", text)
+    assert re.search(r"global_store_dwordx4 .* nt", text)
