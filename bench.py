@@ -21,7 +21,20 @@ cpu_baseline: the CPU oracle (oracle/gdn_oracle.c, a scalar port of the same
 recurrence, one thread) timed on a bounded sample of rows of the same
 workload and scaled to steps/s at B=128.
 
+"paths" (skip with --no-paths) times the other rows of the hot path on their
+BASELINE shapes, each captured in a hipGraph and timed with events:
+  prefill_config2   gdn_prefill_raw, 8 ragged rows of U[64, 1024] tokens, fp16
+                    pool (tokens/s; FP32 flops vs the 157.3 TFLOP/s peak)
+  prefill_tick      gdn_prefill_raw, 4 rows x 256 tokens (config 4's chunks)
+  conv1d_decode     B=64, C=8192, K=4, bf16 in (HBM bytes per the layout)
+  quantize_act      [64, 4096] bf16 (both launches)
+  mixer_step        config 3: 24 GDN layers of quant -> conv -> gated decode at
+                    B=64, one fp16 pool and conv pool per layer
+  mixed_tick        config 4: 4 x 256-token prefill + 96 decode rows on one
+                    192-slot fp16 pool; eager and graph-replayed per bucket
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+                       [--no-paths]
 """
 from __future__ import annotations
 
@@ -54,6 +67,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=512)
     ap.add_argument("--warmup", type=int, default=32)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-paths", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="budget for the CPU-oracle baseline sample")
     return ap.parse_args()
@@ -152,7 +166,7 @@ def cpu_baseline(budget_s):
 
     one_row()
     rows, spent = 0, 0.0
-    while spent < budget_s and rows < 4 * B:
+    while spent < budget_s and rows < 64 * B:
         spent += one_row()
         rows += 1
     per_row = spent / rows
@@ -160,6 +174,174 @@ def cpu_baseline(budget_s):
             "sample": f"{rows} rows of the B=128 step (32 heads, fp16 state emulated, bf16 "
                       f"gates) on the scalar C oracle, {spent:.1f} s, scaled x{B}/rows",
             "host_cpus": os.cpu_count()}
+
+
+FP32_PEAK_TFLOPS = 157.3
+FLOP_PER_TOKEN_HEAD = 7 * 128 * 128   # kv fma, alpha*S, update fma, readout fma (114,688)
+CONV_BYTES_B64 = (64 * 8192 * 3 * 4 + 64 * 8192 * 4 * 4 + 64 * 8192 * 2 + 64 * 8192 * 4
+                  + 8192 * 4 * 4 + 8192 * 4)
+QUANT_BYTES_64x4096 = 64 * 4096 * 2 + 64 * 4096 + 4
+ROW_BYTES = 2 * H * D * D * 2 + (2 * G * D + 2 * H * D) * 4 + H * 2 * 2 + 4
+
+
+def graph_time(torch, fn, reps=5, inner=1, before_replay=None):
+    """Median seconds per call of `fn`, replayed from a captured graph.
+    `before_replay` runs once after capture (e.g. to point padded rows at a
+    scratch slot, which eager validation would refuse as a duplicate)."""
+    fn()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(inner):
+            fn()
+    if before_replay is not None:
+        before_replay()
+    graph.replay()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        graph.replay()
+        b.record()
+        torch.cuda.synchronize()
+        times.append(a.elapsed_time(b) / 1e3 / inner)
+    times.sort()
+    return times[len(times) // 2]
+
+
+def measure_paths(torch, kern):
+    dev = "cuda"
+    g = torch.Generator(device=dev).manual_seed(11)
+    A = -torch.exp(torch.rand(H, generator=g, device=dev) * 2)
+    dtb = torch.rand(H, generator=g, device=dev) * 2 - 1
+    out = {}
+
+    def prefill_case(lens):
+        Bp, T = len(lens), max(lens)
+        pool = (torch.randn(Bp + 4, H, D, D, generator=g, device=dev) * 0.02).half()
+        slots = torch.arange(2, Bp + 2, dtype=torch.int32, device=dev)
+        q = torch.randn(Bp, T, G, D, generator=g, device=dev)
+        k = torch.randn(Bp, T, G, D, generator=g, device=dev)
+        v = torch.randn(Bp, T, H, D, generator=g, device=dev)
+        a = torch.randn(Bp, T, H, generator=g, device=dev)
+        b = torch.randn(Bp, T, H, generator=g, device=dev)
+        y = torch.empty(Bp, T, H, D, device=dev)
+        sl = torch.tensor(lens, dtype=torch.int32, device=dev)
+        t = graph_time(torch, lambda: kern.gdn_prefill_raw(pool, slots, q, k, v, a, b, A, dtb,
+                                                           y, sl), reps=5)
+        tok = sum(lens)
+        tf = tok * H * FLOP_PER_TOKEN_HEAD / t / 1e12
+        return {"rows": Bp, "max_T": T, "tokens": tok, "ms": round(t * 1e3, 3),
+                "tokens_per_s": round(tok / t, 1), "tflops": round(tf, 2),
+                "fp32_frac": round(tf / FP32_PEAK_TFLOPS, 4)}
+
+    lens = torch.randint(64, 1025, (8,), generator=torch.Generator().manual_seed(2)).tolist()
+    out["prefill_config2"] = prefill_case(lens)
+    out["prefill_tick"] = prefill_case([256] * 4)
+
+    # conv1d decode, config 3 shape
+    C = 2 * G * D + H * D
+    conv_pool = torch.randn(72, C, 4, generator=g, device=dev)
+    slots64 = torch.randperm(72, generator=torch.Generator().manual_seed(3))[:64]
+    slots64 = slots64.to(torch.int32).to(dev)
+    w = torch.randn(C, 4, generator=g, device=dev) * 0.1
+    bias = torch.randn(C, generator=g, device=dev) * 0.1
+    xc = torch.randn(64, C, generator=g, device=dev).to(torch.bfloat16)
+    co = torch.empty(64, C, device=dev)
+    t = graph_time(torch, lambda: kern.conv1d_decode(conv_pool, slots64, xc, w, bias, co),
+                   reps=5, inner=20)
+    out["conv1d_decode"] = {"shape": "B=64 C=8192 K=4 bf16", "us": round(t * 1e6, 2),
+                            "gbs": round(CONV_BYTES_B64 / t / 1e9, 1),
+                            "hbm_frac": round(CONV_BYTES_B64 / t / 1e9 / HBM_PEAK_GBS, 4)}
+
+    xq = torch.randn(64, 4096, generator=g, device=dev).to(torch.bfloat16)
+    t = graph_time(torch, lambda: kern.quantize_act(xq), reps=5, inner=20)
+    out["quantize_act"] = {"shape": "64x4096 bf16", "us": round(t * 1e6, 2),
+                           "gbs": round(QUANT_BYTES_64x4096 / t / 1e9, 1)}
+
+    # config 3: 24-layer mixer decode step at B=64
+    L, Bm, S = 24, 64, 72
+    layers = []
+    for _ in range(L):
+        layers.append(dict(
+            pool=(torch.randn(S, H, D, D, generator=g, device=dev) * 0.02).half(),
+            conv=torch.randn(S, C, 4, generator=g, device=dev) * 0.5,
+            w=torch.randn(C, 4, generator=g, device=dev) * 0.1,
+            bias=torch.randn(C, generator=g, device=dev) * 0.1,
+            x=torch.randn(Bm, 4096, generator=g, device=dev).to(torch.bfloat16),
+            xin=torch.randn(Bm, C, generator=g, device=dev).to(torch.bfloat16),
+            a=torch.randn(Bm, H, generator=g, device=dev).to(torch.bfloat16),
+            b=torch.randn(Bm, H, generator=g, device=dev).to(torch.bfloat16),
+            cout=torch.empty(Bm, C, device=dev), y=torch.empty(Bm, H, D, device=dev)))
+
+    def mixer_step():
+        for ly in layers:
+            kern.quantize_act(ly["x"])
+            kern.conv1d_decode(ly["conv"], slots64, ly["xin"], ly["w"], ly["bias"], ly["cout"])
+            q, k, v = torch.split(ly["cout"], [G * D, G * D, H * D], dim=-1)
+            kern.gdn_decode_raw(ly["pool"], slots64, q.unflatten(-1, (G, D)),
+                                k.unflatten(-1, (G, D)), v.unflatten(-1, (H, D)), ly["a"],
+                                ly["b"], A, dtb, ly["y"])
+
+    t = graph_time(torch, mixer_step, reps=5)
+    step_bytes = L * (QUANT_BYTES_64x4096 + CONV_BYTES_B64 + Bm * ROW_BYTES)
+    out["mixer_step"] = {"layers": L, "batch": Bm, "us": round(t * 1e6, 1),
+                         "gbs": round(step_bytes / t / 1e9, 1),
+                         "hbm_frac": round(step_bytes / t / 1e9 / HBM_PEAK_GBS, 4),
+                         "bytes": step_bytes}
+    del layers
+
+    # config 4: mixed tick on one 192-slot fp16 pool
+    pool = (torch.randn(192, H, D, D, generator=g, device=dev) * 0.02).half()
+    pre_slots = torch.arange(96, 100, dtype=torch.int32, device=dev)
+    pq = torch.randn(4, 256, G, D, generator=g, device=dev)
+    pk = torch.randn(4, 256, G, D, generator=g, device=dev)
+    pv = torch.randn(4, 256, H, D, generator=g, device=dev)
+    pa = torch.randn(4, 256, H, generator=g, device=dev).to(torch.bfloat16)
+    pb = torch.randn(4, 256, H, generator=g, device=dev).to(torch.bfloat16)
+    py = torch.empty(4, 256, H, D, device=dev)
+    plen = torch.full((4,), 256, dtype=torch.int32, device=dev)
+    tick = {}
+    for bucket in (16, 32, 64, 96, 128):
+        live = min(bucket, 96)
+        # captured with distinct slots; pad rows then point at scratch slot 191
+        sl = torch.arange(bucket, dtype=torch.int32, device=dev)
+        padded = torch.cat([torch.arange(live, dtype=torch.int32, device=dev),
+                            torch.full((bucket - live,), 191, dtype=torch.int32, device=dev)])
+        dq = torch.randn(bucket, G, D, generator=g, device=dev)
+        dk = torch.randn(bucket, G, D, generator=g, device=dev)
+        dv = torch.randn(bucket, H, D, generator=g, device=dev)
+        da = torch.randn(bucket, H, generator=g, device=dev).to(torch.bfloat16)
+        db = torch.randn(bucket, H, generator=g, device=dev).to(torch.bfloat16)
+        dy = torch.empty(bucket, H, D, device=dev)
+
+        def tick_fn():
+            kern.gdn_prefill_raw(pool, pre_slots, pq, pk, pv, pa, pb, A, dtb, py, plen)
+            kern.gdn_decode_raw(pool, sl, dq, dk, dv, da, db, A, dtb, dy)
+
+        entry = {"graph_us": round(graph_time(torch, tick_fn, reps=5,
+                                              before_replay=lambda: sl.copy_(padded)) * 1e6, 1)}
+        if bucket <= 96:  # eager needs distinct slots (no scratch padding)
+            tick_fn()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(5):
+                tick_fn()
+            torch.cuda.synchronize()
+            entry["eager_us"] = round((time.perf_counter() - t0) / 5 * 1e6, 1)
+        tick[str(bucket)] = entry
+    tick_bytes = 96 * ROW_BYTES + 4 * 2 * H * D * D * 2 + 4 * 256 * (
+        (2 * G * D + 2 * H * D) * 4 + H * 2 * 2)
+    tick["bytes_b96"] = tick_bytes
+    tick["gbs_b96_graph"] = round(tick_bytes / (tick["96"]["graph_us"] * 1e-6) / 1e9, 1)
+    out["mixed_tick"] = tick
+    return out
 
 
 def main():
@@ -214,6 +396,8 @@ def main():
         "copy_gbs": round(copy_gbs, 1),
         "bytes_per_step": STEP_BYTES,
     }
+    if not args.no_paths:
+        out["paths"] = measure_paths(torch, kern)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(out), flush=True)

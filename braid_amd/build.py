@@ -52,31 +52,34 @@ def common_flags() -> list[str]:
     ]
 
 
-def _compile(src: str) -> Path:
-    OBJ_DIR.mkdir(exist_ok=True)
-    out = OBJ_DIR / (Path(src).stem + ".o")
+def _compile(src: str, defines: tuple = (), obj_dir: Path = OBJ_DIR) -> Path:
+    obj_dir.mkdir(parents=True, exist_ok=True)
+    out = obj_dir / (Path(src).stem + ".o")
     lang = ["-x", "hip"] if src.endswith(".hip") else []
-    cmd = [hipcc(), *common_flags(), *lang, "-c", str(CSRC / src), "-o", str(out)]
+    cmd = [hipcc(), *common_flags(), *[f"-D{d}" for d in defines], *lang, "-c",
+           str(CSRC / src), "-o", str(out)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src}:\n{' '.join(cmd)}\n{r.stdout}{r.stderr}")
     return out
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile every source and link the shared library. Always rebuilds."""
+def build(verbose: bool = False, defines: tuple = (), lib: Path = LIB) -> Path:
+    """Compile every source and link the shared library. Always rebuilds.
+    `defines` (NAME=VALUE strings) and `lib` select a tuning variant."""
+    obj_dir = OBJ_DIR if lib == LIB else lib.parent / (lib.stem + "_obj")
     with ThreadPoolExecutor(max_workers=min(4, len(SOURCES))) as ex:
-        objs = list(ex.map(_compile, SOURCES))
-    tmp = LIB.with_suffix(".so.tmp")
+        objs = list(ex.map(lambda s: _compile(s, defines, obj_dir), SOURCES))
+    tmp = lib.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs),
            "-o", str(tmp)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{' '.join(cmd)}\n{r.stdout}{r.stderr}")
-    os.replace(tmp, LIB)
+    os.replace(tmp, lib)
     if verbose:
-        print(f"built {LIB}")
-    return LIB
+        print(f"built {lib}")
+    return lib
 
 
 if __name__ == "__main__":

@@ -22,13 +22,15 @@ struct Storage<F16> { using T = uint16_t; };
 template <>
 struct Storage<BF16> { using T = uint16_t; };
 
+// One decode token for the tile (blockIdx.x = b * H + h).
 template <class Tag, class Gates>
-__global__ void __launch_bounds__(kTileThreads)
-gdn_decode_kernel(typename Storage<Tag>::T* __restrict__ pool,
-                  const int* __restrict__ slot_idx,
-                  const float* __restrict__ q, const float* __restrict__ k,
-                  const float* __restrict__ v, Gates gates, float* __restrict__ y,
-                  int H, int heads_per_group, long q_row, long k_row, long v_row) {
+__device__ __forceinline__ void decode_tile(typename Storage<Tag>::T* __restrict__ pool,
+                                            const int* __restrict__ slot_idx,
+                                            const float* __restrict__ q,
+                                            const float* __restrict__ k,
+                                            const float* __restrict__ v, const Gates& gates,
+                                            float* __restrict__ y, int H, int heads_per_group,
+                                            long q_row, long k_row, long v_row) {
   using ST = typename Storage<Tag>::T;
   const int b = blockIdx.x / H;
   const int h = blockIdx.x - b * H;
@@ -51,16 +53,25 @@ gdn_decode_kernel(typename Storage<Tag>::T* __restrict__ pool,
   QK qk;
   normalize_qk(L, q + (size_t)b * q_row + (size_t)g * kSS,
                k + (size_t)b * k_row + (size_t)g * kSS, qk);
-  float a, bt;
-  gates.get(b, h, 0, H, 1, a, bt);
+  publish_gates(L, gates, gates.load(b, h, 0, H, 1), h, lds);
 
   float yy[8];
-  gdn_token<Tag>(L, S, qk, vv, a, bt, lds, yy);
+  gdn_token<Tag>(L, S, qk, vv, lds, yy);
 
 #pragma unroll
   for (int i = 0; i < kRowsPerLane; ++i) S[i].store_nt(tile + (size_t)L.row(i) * kHD);
-  // Each column chunk's totals sit in all 16 of its lanes; wave w writes chunks 4w..4w+3.
-  if (L.rg == 0 && (L.c8 >> 2) == L.wave) store8(y + ((size_t)b * H + h) * kHD + L.col0, yy);
+  // Each column chunk's totals sit in all its lanes; one lane per chunk writes them.
+  if (stores_y(L)) store8(y + ((size_t)b * H + h) * kHD + L.col0, yy);
+}
+
+template <class Tag, class Gates>
+__global__ void __launch_bounds__(kTileThreads)
+gdn_decode_kernel(typename Storage<Tag>::T* __restrict__ pool, const int* __restrict__ slot_idx,
+                  const float* __restrict__ q, const float* __restrict__ k,
+                  const float* __restrict__ v, Gates gates, float* __restrict__ y, int H,
+                  int heads_per_group, long q_row, long k_row, long v_row) {
+  decode_tile<Tag, Gates>(pool, slot_idx, q, k, v, gates, y, H, heads_per_group, q_row, k_row,
+                          v_row);
 }
 
 template <class Tag, class Gates>
@@ -84,17 +95,40 @@ gdn_prefill_kernel(typename Storage<Tag>::T* __restrict__ pool,
 #pragma unroll
   for (int i = 0; i < kRowsPerLane; ++i) S[i].load_nt(tile + (size_t)L.row(i) * kHD);
 
+  // Software pipeline: token t + 1's inputs are loaded, its q/k normalised and
+  // its gates computed while token t's recurrence runs; none of them depends
+  // on the state, so the serial chain per token is the recurrence alone.
+  QK qk;
+  float vv[8];
+  if (T > 0) {
+    QKRaw raw;
+    load_qk(L, q + ((size_t)b * T * G + g) * kSS, k + ((size_t)b * T * G + g) * kSS, raw);
+    load8(v + ((size_t)b * T * H + h) * kHD + L.col0, vv);
+    publish_gates(L, gates, gates.load(b, h, 0, H, T), h, lds);
+    normalize_qk(raw, qk);
+  }
   for (int t = 0; t < T; ++t) {
     const size_t bt_idx = (size_t)b * T + t;
-    float vv[8];
-    load8(v + (bt_idx * H + h) * kHD + L.col0, vv);
-    QK qk;
-    normalize_qk(L, q + (bt_idx * G + g) * kSS, k + (bt_idx * G + g) * kSS, qk);
-    float a, bt;
-    gates.get(b, h, t, H, T, a, bt);
+    const bool more = t + 1 < T;
+    QKRaw raw_n;
+    GateRaw gate_n{};
+    float vv_n[8];
+    if (more) {
+      load_qk(L, q + ((bt_idx + 1) * G + g) * kSS, k + ((bt_idx + 1) * G + g) * kSS, raw_n);
+      load8(v + ((bt_idx + 1) * H + h) * kHD + L.col0, vv_n);
+      gate_n = gates.load(b, h, t + 1, H, T);
+    }
     float yy[8];
-    gdn_token<Tag>(L, S, qk, vv, a, bt, lds, yy);
-    if (L.rg == 0 && (L.c8 >> 2) == L.wave) store8(y + (bt_idx * H + h) * kHD + L.col0, yy);
+    gdn_token<Tag>(L, S, qk, vv, lds, yy);
+    if (stores_y(L)) store8(y + (bt_idx * H + h) * kHD + L.col0, yy);
+    if (more) {
+      // lds.gate was last read before this token's second barrier: safe to
+      // overwrite; the next token's first barrier publishes the new values.
+      publish_gates(L, gates, gate_n, h, lds);
+      normalize_qk(raw_n, qk);
+#pragma unroll
+      for (int c = 0; c < 8; ++c) vv[c] = vv_n[c];
+    }
   }
 
 #pragma unroll

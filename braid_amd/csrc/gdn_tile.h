@@ -5,22 +5,23 @@
 // the pool layout [n_slots, H, SS, HD] of braid/model/cache.py:127-128. A row
 // is 256 bytes of an fp16 pool.
 //
-// A tile belongs to one 256-thread workgroup: wave w owns the 32 full rows
-// [32w, 32w + 32). Lane l of a wave owns the 8-column chunk c8 = l % 16 of rows
-// 32w + r + 4i (r = l / 16, i = 0..7), so each of a lane's eight state accesses
-// is one 16-byte vector and every wave-wide load or store instruction covers
-// four consecutive rows — 1 KiB contiguous for fp16. Measured on MI355X, this
-// whole-row pattern streams ~10% faster than per-wave column panels, and the
-// state goes through nontemporal loads and stores (it is touched once per
-// step and never re-read by the step).
+// A tile belongs to one workgroup of kWaves = 4 waves (256 threads): wave w
+// owns the 32 full rows [32w, 32w + 32). Lane l of a wave owns the 8-column
+// chunk c8 = l % 16 of rows 32w + r + 4i (r = l / 16, i = 0..7), so each of a
+// lane's eight state accesses is one 16-byte vector and every wave-wide load
+// or store instruction covers four consecutive rows — 1 KiB contiguous for
+// fp16. Measured on MI355X, this whole-row pattern streams ~18% faster than
+// per-wave column panels, and the state goes through nontemporal loads and
+// stores (it is touched once per step and never re-read by the step).
 //
 // Every reduction of the recurrence runs over rows s for a fixed column d, in
 // one fixed order that defines the result's bits:
 //   1. sequentially over a lane's eight rows (an fma chain, i = 0..7);
 //   2. a butterfly over the four row groups r of a wave (lane xor 16, then xor
 //      32): partners add the same two operands, so all lanes agree bitwise;
-//   3. across the four waves through LDS, summed as (w0 + w1) + (w2 + w3) by
-//      every lane that needs the total.
+//   3. across the four waves through LDS, as the pairwise tree
+//      (w0 + w1) + (w2 + w3), evaluated the same way by every lane that needs
+//      the total.
 //
 // The state lives in registers in its STORAGE type. Each token widens it to
 // fp32, runs the recurrence in fp32 and narrows it back, exactly as a decode
@@ -46,11 +47,15 @@ namespace braid {
 
 constexpr int kSS = 128;                          // key dim (state rows)
 constexpr int kHD = 128;                          // value dim (state columns)
-constexpr int kWaves = 4;                         // waves per tile
+#ifndef BRAID_TILE_WAVES
+#define BRAID_TILE_WAVES 4
+#endif
+constexpr int kWaves = BRAID_TILE_WAVES;          // waves per tile (4 or 8)
 constexpr int kRowsPerWave = kSS / kWaves;        // 32
 constexpr int kChunks = kHD / 8;                  // 16 eight-column chunks per row
 constexpr int kRowGroups = 64 / kChunks;          // 4 row groups per wave
 constexpr int kRowsPerLane = kRowsPerWave / kRowGroups;  // 8
+constexpr int kChunksPerWave = kChunks / kWaves;  // y chunks each wave stores
 constexpr int kTileThreads = 64 * kWaves;
 constexpr float kL2Eps = 1e-6f;
 // 128^-0.5 correctly rounded to fp32 (0x3DB504F3).
@@ -69,6 +74,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // fp32 -> bf16 bits, round to nearest even; NaN -> 0x7FC0 (a quiet NaN).
+// Used for the activation-dtype round trip of the gates.
 __device__ __forceinline__ uint32_t bf16_bits_rne(float f) {
   const uint32_t u = __float_as_uint(f);
   if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
@@ -77,19 +83,27 @@ __device__ __forceinline__ uint32_t bf16_bits_rne(float f) {
 __device__ __forceinline__ float bf16_widen(uint32_t bits16) {
   return __uint_as_float(bits16 << 16);
 }
-// fp32 -> fp16 bits, round to nearest even, of the ALREADY ROUNDED fp32 value.
-// The empty asm pins `f` in a register: without it the compiler may fuse
-// fptrunc(fma(a, b, c)) into one mixed-precision fma that rounds straight to
-// fp16 (a single rounding instead of fp32-then-fp16). That is a different
-// result in rare ties, and the compiler makes the choice per call site, so
-// decode and prefill could disagree. The reference narrows the fp32 value
-// (gdn_decode.cu:29-30); so does this.
-__device__ __forceinline__ uint32_t f16_bits_rne(float f) {
-  asm volatile("" : "+v"(f));
-  return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f);
-}
 __device__ __forceinline__ float f16_widen(uint32_t bits16) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
+}
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// Two already-rounded fp32 values -> packed 16-bit pair, round to nearest
+// even: one v_cvt_pk_f16_f32 / v_cvt_pk_bf16_f32 on gfx950. Written as a
+// vector conversion on purpose: the scalar spelling (_Float16)fmaf(...) lets
+// the compiler fuse the fma and the narrowing into one mixed-precision fma
+// that rounds ONCE, straight to fp16, which differs in rare ties from the
+// reference's fp32-then-narrow (gdn_decode.cu:29-30) and is chosen per call
+// site (it broke decode == prefill bit-identity). The packed conversion
+// consumes the rounded fp32 results.
+__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, f16x2));
+}
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, bf16x2));
 }
 
 template <class Tag>
@@ -108,12 +122,18 @@ struct Row8<F32> {
     __builtin_nontemporal_store(hi, reinterpret_cast<f32x4*>(p + 4));
   }
   __device__ __forceinline__ float get(int c) const { return c < 4 ? lo[c] : hi[c - 4]; }
-  __device__ __forceinline__ void set(int c, float x) {
-    if (c < 4) lo[c] = x; else hi[c - 4] = x;
+  // Columns c and c + 1 (c even).
+  __device__ __forceinline__ void set2(int c, float x0, float x1) {
+    if (c < 4) {
+      lo[c] = x0;
+      lo[c + 1] = x1;
+    } else {
+      hi[c - 4] = x0;
+      hi[c - 3] = x1;
+    }
   }
 };
 
-template <class Tag>
 struct Row8Half {
   using elem = uint16_t;
   u32x4 raw;  // element c sits in bits 16*(c&1) of raw[c>>1]
@@ -126,22 +146,22 @@ struct Row8Half {
   __device__ __forceinline__ uint32_t bits(int c) const {
     return (raw[c >> 1] >> (16 * (c & 1))) & 0xffffu;
   }
-  __device__ __forceinline__ void put(int c, uint32_t b) {
-    const int w = c >> 1, sh = 16 * (c & 1);
-    raw[w] = (raw[w] & ~(0xffffu << sh)) | (b << sh);
+};
+
+template <>
+struct Row8<F16> : Row8Half {
+  __device__ __forceinline__ float get(int c) const { return f16_widen(bits(c)); }
+  __device__ __forceinline__ void set2(int c, float x0, float x1) {
+    raw[c >> 1] = pack_f16x2(x0, x1);
   }
 };
 
 template <>
-struct Row8<F16> : Row8Half<F16> {
-  __device__ __forceinline__ float get(int c) const { return f16_widen(bits(c)); }
-  __device__ __forceinline__ void set(int c, float x) { put(c, f16_bits_rne(x)); }
-};
-
-template <>
-struct Row8<BF16> : Row8Half<BF16> {
+struct Row8<BF16> : Row8Half {
   __device__ __forceinline__ float get(int c) const { return bf16_widen(bits(c)); }
-  __device__ __forceinline__ void set(int c, float x) { put(c, bf16_bits_rne(x)); }
+  __device__ __forceinline__ void set2(int c, float x0, float x1) {
+    raw[c >> 1] = pack_bf16x2(x0, x1);
+  }
 };
 
 // ---------------------------------------------------------------------------
@@ -170,16 +190,25 @@ __device__ __forceinline__ float rowgroup_sum(float v) {
 // ---------------------------------------------------------------------------
 // Gate policies: where (alpha, beta) for (row b, head h, token t) come from.
 
+// Each policy splits into load() — the global reads for (row b, head h,
+// token t) — and eval_alpha() / eval_beta() — the arithmetic — so a scan can issue the
+// next token's reads early, and so one wave can evaluate each gate for the
+// whole tile (publish_gates).
+struct GateRaw {
+  float x0, x1;  // policy-defined raw values
+  bool pad;      // a pad column: alpha = 1, beta = 0
+};
+
 // Gates the caller computed (gdn_decode.cu:102-110): [B, T, H] fp32.
 struct PrecomputedGates {
   const float* alpha;
   const float* beta;
-  __device__ __forceinline__ void get(int b, int h, int t, int H, int T, float& a,
-                                      float& bt) const {
+  __device__ __forceinline__ GateRaw load(int b, int h, int t, int H, int T) const {
     const size_t i = ((size_t)b * T + t) * H + h;
-    a = alpha[i];
-    bt = beta[i];
+    return GateRaw{alpha[i], beta[i], false};
   }
+  __device__ __forceinline__ float eval_alpha(const GateRaw& r, int) const { return r.x0; }
+  __device__ __forceinline__ float eval_beta(const GateRaw& r) const { return r.x1; }
 };
 
 template <class ActTag>
@@ -213,26 +242,28 @@ struct RawGates {
   const float* A;
   const float* dt_bias;
   const int* seq_lens;  // nullptr: every column live
-  __device__ __forceinline__ void get(int b, int h, int t, int H, int T, float& a,
-                                      float& bt) const {
-    if (seq_lens != nullptr && t >= seq_lens[b]) {
-      a = 1.f;
-      bt = 0.f;
-      return;
-    }
+  __device__ __forceinline__ GateRaw load(int b, int h, int t, int H, int T) const {
+    if (seq_lens != nullptr && t >= seq_lens[b]) return GateRaw{0.f, 0.f, true};
     const size_t i = ((size_t)b * T + t) * H + h;
-    const float e = expf(-ActRead<ActTag>::widen(b_raw[i]));
-    bt = ActRead<ActTag>::round_trip(1.f / (1.f + e));
-    const float x = ActRead<ActTag>::widen(a_raw[i]) + dt_bias[h];
+    return GateRaw{ActRead<ActTag>::widen(a_raw[i]), ActRead<ActTag>::widen(b_raw[i]), false};
+  }
+  __device__ __forceinline__ float eval_alpha(const GateRaw& r, int h) const {
+    if (r.pad) return 1.f;
+    const float x = r.x0 + dt_bias[h];
     const float sp = x > 20.f ? x : log1pf(expf(x));
-    a = expf(A[h] * sp);
+    return expf(A[h] * sp);
+  }
+  __device__ __forceinline__ float eval_beta(const GateRaw& r) const {
+    if (r.pad) return 0.f;
+    const float e = expf(-r.x1);
+    return ActRead<ActTag>::round_trip(1.f / (1.f + e));
   }
 };
 
 // ---------------------------------------------------------------------------
 // Lane geometry within a tile.
 struct LaneMap {
-  int wave;  // 0..3: rows [32 wave, 32 wave + 32)
+  int wave;  // 0..kWaves-1: rows [kRowsPerWave wave, kRowsPerWave (wave + 1))
   int lane;  // 0..63
   int rg;    // row group 0..3
   int c8;    // column chunk 0..15
@@ -255,41 +286,59 @@ struct LaneMap {
 struct TileLds {
   float kv[kWaves][kHD];
   float y[kWaves][kHD];
+  float gate[2];  // this token's alpha, beta (see publish_gates)
 };
 
 // q_hat / k_hat for this lane's rows, from the dense [SS] fp32 key-group
 // vectors. Every lane of every wave computes the norms with the same reduction
-// tree, so every wave sees identical bits.
+// tree, so every wave sees identical bits. Split into the loads (QKRaw) and
+// the arithmetic (normalize_qk) so a scan can issue the next token's loads
+// before it runs the current token.
 struct QK {
   float qh[kRowsPerLane];
   float kh[kRowsPerLane];
 };
 
-__device__ __forceinline__ void normalize_qk(const LaneMap& L, const float* __restrict__ q,
-                                             const float* __restrict__ k, QK& out) {
-  const float2 q2 = *reinterpret_cast<const float2*>(q + 2 * L.lane);
-  const float2 k2 = *reinterpret_cast<const float2*>(k + 2 * L.lane);
-  float qr[kRowsPerLane], kr[kRowsPerLane];
+struct QKRaw {
+  float2 q2, k2;                   // elements 2 lane, 2 lane + 1 (for the norms)
+  float qr[kRowsPerLane];          // this lane's rows
+  float kr[kRowsPerLane];
+};
+
+__device__ __forceinline__ void load_qk(const LaneMap& L, const float* __restrict__ q,
+                                        const float* __restrict__ k, QKRaw& r) {
+  r.q2 = *reinterpret_cast<const float2*>(q + 2 * L.lane);
+  r.k2 = *reinterpret_cast<const float2*>(k + 2 * L.lane);
 #pragma unroll
   for (int i = 0; i < kRowsPerLane; ++i) {
-    qr[i] = q[L.row(i)];
-    kr[i] = k[L.row(i)];
+    r.qr[i] = q[L.row(i)];
+    r.kr[i] = k[L.row(i)];
   }
-  const float qs = wave_sum(q2.x * q2.x + q2.y * q2.y);
-  const float ks = wave_sum(k2.x * k2.x + k2.y * k2.y);
+}
+
+__device__ __forceinline__ void normalize_qk(const QKRaw& r, QK& out) {
+  const float qs = wave_sum(r.q2.x * r.q2.x + r.q2.y * r.q2.y);
+  const float ks = wave_sum(r.k2.x * r.k2.x + r.k2.y * r.k2.y);
   const float q_inv = rsqrtf(qs + kL2Eps);
   const float k_inv = rsqrtf(ks + kL2Eps);
 #pragma unroll
   for (int i = 0; i < kRowsPerLane; ++i) {
-    out.qh[i] = qr[i] * q_inv;
-    out.kh[i] = kr[i] * k_inv;
+    out.qh[i] = r.qr[i] * q_inv;
+    out.kh[i] = r.kr[i] * k_inv;
   }
+}
+
+__device__ __forceinline__ void normalize_qk(const LaneMap& L, const float* __restrict__ q,
+                                             const float* __restrict__ k, QK& out) {
+  QKRaw r;
+  load_qk(L, q, k, r);
+  normalize_qk(r, out);
 }
 
 // Completes a column sum: the lane's chain value `part` for columns
 // col0..col0+7 is reduced over the wave's row groups, exchanged through `buf`
-// and summed over the four waves in the fixed order (w0 + w1) + (w2 + w3).
-// Every lane returns the eight column totals of its chunk.
+// and summed over the waves by a fixed pairwise tree. Every lane returns the
+// eight column totals of its chunk.
 __device__ __forceinline__ void tile_column_sums(const LaneMap& L, float (&part)[8],
                                                  float (*buf)[kHD]) {
 #pragma unroll
@@ -317,17 +366,34 @@ __device__ __forceinline__ void tile_column_sums(const LaneMap& L, float (&part)
     }
   }
 #pragma unroll
-  for (int c = 0; c < 8; ++c) part[c] = (w[0][c] + w[1][c]) + (w[2][c] + w[3][c]);
+  for (int c = 0; c < 8; ++c) {
+    float lvl[kWaves];
+#pragma unroll
+    for (int j = 0; j < kWaves; ++j) lvl[j] = w[j][c];
+#pragma unroll
+    for (int n = kWaves; n > 1; n >>= 1) {
+#pragma unroll
+      for (int j = 0; j < n / 2; ++j) lvl[j] = lvl[2 * j] + lvl[2 * j + 1];
+    }
+    part[c] = lvl[0];
+  }
+}
+
+// True for the lanes that write a column chunk's outputs: row group 0 of the
+// wave assigned to that chunk (each wave stores kChunksPerWave chunks).
+__device__ __forceinline__ bool stores_y(const LaneMap& L) {
+  return L.rg == 0 && L.c8 / kChunksPerWave == L.wave;
 }
 
 // One token of the recurrence on this lane's 8 x 8 block. `v` holds the eight
 // value entries of the lane's columns; `y` receives their outputs (identical
-// in every lane of a column chunk). Contains two workgroup barriers, so all
-// four waves of the tile must call it together.
+// in every lane of a column chunk). alpha and beta are read from lds.gate
+// after the first barrier (publish_gates writes them before it). Contains two
+// workgroup barriers, so all waves of the tile must call it together.
 template <class Tag>
 __device__ __forceinline__ void gdn_token(const LaneMap& L, Row8<Tag> (&S)[kRowsPerLane],
-                                          const QK& qk, const float (&v)[8], float alpha,
-                                          float beta, TileLds& lds, float (&y)[8]) {
+                                          const QK& qk, const float (&v)[8], TileLds& lds,
+                                          float (&y)[8]) {
   float kv[8];
 #pragma unroll
   for (int c = 0; c < 8; ++c) kv[c] = S[0].get(c) * qk.kh[0];
@@ -337,6 +403,8 @@ __device__ __forceinline__ void gdn_token(const LaneMap& L, Row8<Tag> (&S)[kRows
     for (int c = 0; c < 8; ++c) kv[c] = fmaf(S[i].get(c), qk.kh[i], kv[c]);
   }
   tile_column_sums(L, kv, lds.kv);
+  const float alpha = lds.gate[0];
+  const float beta = lds.gate[1];
   float delta[8];
 #pragma unroll
   for (int c = 0; c < 8; ++c) delta[c] = (v[c] - alpha * kv[c]) * beta;
@@ -347,15 +415,34 @@ __device__ __forceinline__ void gdn_token(const LaneMap& L, Row8<Tag> (&S)[kRows
 #pragma unroll
   for (int i = 0; i < kRowsPerLane; ++i) {
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      const float nv = fmaf(qk.kh[i], delta[c], alpha * S[i].get(c));
-      S[i].set(c, nv);
-      acc[c] = fmaf(nv, qk.qh[i], acc[c]);
+    for (int c = 0; c < 8; c += 2) {
+      const float n0 = fmaf(qk.kh[i], delta[c], alpha * S[i].get(c));
+      const float n1 = fmaf(qk.kh[i], delta[c + 1], alpha * S[i].get(c + 1));
+      S[i].set2(c, n0, n1);
+      acc[c] = fmaf(n0, qk.qh[i], acc[c]);
+      acc[c + 1] = fmaf(n1, qk.qh[i], acc[c + 1]);
     }
   }
   tile_column_sums(L, acc, lds.y);
 #pragma unroll
   for (int c = 0; c < 8; ++c) y[c] = acc[c] * kYScale;
+}
+
+// Computes one token's gates ONCE per tile and leaves them in lds.gate for
+// gdn_token: wave 0 evaluates alpha (exp, log1p, exp), wave 1 beta (exp and a
+// divide), each from the raw values all waves loaded. The next workgroup
+// barrier publishes them. The arithmetic is the policy's own (Gates::eval_alpha /
+// Gates::eval_beta), so which wave runs it does not change a bit.
+template <class Gates>
+__device__ __forceinline__ void publish_gates(const LaneMap& L, const Gates& gates,
+                                              const GateRaw& r, int h, TileLds& lds) {
+  if (L.wave == 0) {
+    const float a = gates.eval_alpha(r, h);
+    if (L.lane == 0) lds.gate[0] = a;
+  } else if (L.wave == 1) {
+    const float bt = gates.eval_beta(r);
+    if (L.lane == 0) lds.gate[1] = bt;
+  }
 }
 
 __device__ __forceinline__ void load8(const float* __restrict__ p, float (&out)[8]) {

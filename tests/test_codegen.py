@@ -60,6 +60,14 @@ def test_no_scalar_memory_writes(asm, src):
     assert not bad, bad
 
 
+@pytest.mark.parametrize("src", SOURCES)
+def test_no_kernel_spills_to_scratch(asm, src):
+    """A spill in a bandwidth-bound kernel is extra memory traffic; the
+    occupancy chosen for every kernel must fit its registers."""
+    sizes = re.findall(r"\.amdhsa_private_segment_fixed_size\s+(\d+)", asm[src])
+    assert sizes and all(int(x) == 0 for x in sizes), sizes
+
+
 def test_decode_state_uses_128_bit_nontemporal_accesses(asm):
     text = asm["gdn_scan.hip"]
     assert re.search(r"global_load_dwordx4 .* nt", text)

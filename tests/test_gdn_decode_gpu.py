@@ -261,3 +261,29 @@ def test_replay_with_rotating_slots_is_cheap(kern):
     ms = (time.perf_counter() - t) / 200 * 1e3
     print(f"\n  rotating replay {ms:.4f} ms/step")
     assert ms < 1.0
+
+
+@pytest.mark.parametrize("dt", POOL_DTYPES, ids=POOL_IDS)
+def test_state_narrowing_rounds_to_nearest_even_exactly(kern, dt):
+    """With beta = 0 the new state is exactly fl32(alpha * S) (the update adds a
+    signed zero), narrowed once to the pool type. That value is fixed by IEEE
+    arithmetic, so the pool must match it BITWISE: a truncating or otherwise
+    mis-rounding narrowing fails here, where the 1-ulp oracle bars could not
+    see it."""
+    B, H = 4, 8
+    p = pool(B, H=H, dtype=dt, seed=17, scale=1.0)
+    before = p.float().cpu().numpy()
+    inp = decode_inputs(B, H=H, seed=18)
+    inp["beta"].zero_()
+    y = torch.empty(B, H, 128, device=DEV)
+    kern.gdn_decode(p, torch.arange(B, dtype=torch.int32, device=DEV), inp["q"], inp["k"],
+                    inp["v"], inp["alpha"], inp["beta"], y)
+    prod = (before * inp["alpha"].cpu().numpy()[:, :, None, None]).astype(np.float32)
+    expected = oracle.narrow(prod, KIND[dt])
+    got = to_np_pool(p)
+    if dt == torch.float32:
+        assert np.array_equal(got, expected)
+    else:
+        assert np.array_equal(got.view(np.uint16), expected.view(np.uint16)), (
+            f"{int((got.view(np.uint16) != expected.view(np.uint16)).sum())} elements "
+            "rounded differently from round-to-nearest-even")
