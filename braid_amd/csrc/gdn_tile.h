@@ -35,7 +35,7 @@
 //   q_hat = q * rsqrt(sum q^2 + 1e-6), k_hat likewise (HF additive epsilon)
 //   kv[d]    = sum_s S[s,d] k_hat[s]              (undecayed state)
 //   delta[d] = (v[d] - alpha * kv[d]) * beta
-//   S'[s,d]  = alpha * S[s,d] + k_hat[s] * delta[d]
+//   S'[s,d]  = alpha * S[s,d] + k_hat[s] * delta[d]   (as fma(alpha, S, k_hat*delta))
 //   y[d]     = (sum_s S'[s,d] q_hat[s]) * 128^-0.5  (fp32 S', before narrowing)
 // Head h reads key group g = h / (H / G) (grouped layout, gdn_decode.cu:173).
 #pragma once
@@ -416,8 +416,11 @@ __device__ __forceinline__ void gdn_token(const LaneMap& L, Row8<Tag> (&S)[kRows
   for (int i = 0; i < kRowsPerLane; ++i) {
 #pragma unroll
     for (int c = 0; c < 8; c += 2) {
-      const float n0 = fmaf(qk.kh[i], delta[c], alpha * S[i].get(c));
-      const float n1 = fmaf(qk.kh[i], delta[c + 1], alpha * S[i].get(c + 1));
+      // S' = alpha * S + k_hat * delta, contracted as fma(alpha, S, k_hat * delta):
+      // the 16-bit S feeds the fma directly (v_fma_mix, exact widening), one
+      // instruction fewer per element than widening, scaling, then fusing.
+      const float n0 = fmaf(alpha, S[i].get(c), qk.kh[i] * delta[c]);
+      const float n1 = fmaf(alpha, S[i].get(c + 1), qk.kh[i] * delta[c + 1]);
       S[i].set2(c, n0, n1);
       acc[c] = fmaf(n0, qk.qh[i], acc[c]);
       acc[c + 1] = fmaf(n1, qk.qh[i], acc[c + 1]);
