@@ -26,6 +26,8 @@ BASELINE shapes, each captured in a hipGraph and timed with events:
   prefill_config2   gdn_prefill_raw, 8 ragged rows of U[64, 1024] tokens, fp16
                     pool (tokens/s; FP32 flops vs the 157.3 TFLOP/s peak)
   prefill_tick      gdn_prefill_raw, 4 rows x 256 tokens (config 4's chunks)
+  conv1d_prefill_config2  the chunked causal conv before config 2's scan
+                    (bytes: bf16 x in, fp32 out over the padded [8, T, 8192])
   conv1d_decode     B=64, C=8192, K=4, bf16 in (HBM bytes per the layout)
   quantize_act      [64, 4096] bf16 (both launches)
   mixer_step        config 3: 24 GDN layers of quant -> conv -> gated decode at
@@ -243,6 +245,23 @@ def measure_paths(torch, kern):
 
     lens = torch.randint(64, 1025, (8,), generator=torch.Generator().manual_seed(2)).tolist()
     out["prefill_config2"] = prefill_case(lens)
+
+    # config 2's causal conv prefill: 8 ragged rows, C=8192, K=4, bf16 in, fp32 out
+    Cc, Tm = 2 * G * D + H * D, max(lens)
+    cpool = torch.zeros(12, Cc, 4, device=dev)
+    cslots = torch.arange(8, dtype=torch.int32, device=dev)
+    cx = torch.randn(8, Tm, Cc, generator=g, device=dev).to(torch.bfloat16)
+    cw = torch.randn(Cc, 4, generator=g, device=dev) * 0.1
+    cout = torch.empty(8, Tm, Cc, device=dev)
+    clens = torch.tensor(lens, dtype=torch.int32, device=dev)
+    t = graph_time(torch, lambda: kern.conv1d_prefill(cpool, cslots, cx, cw, None, cout, clens),
+                   reps=5)
+    cbytes = 8 * Tm * Cc * (2 + 4) + 2 * 8 * Cc * 4 * 4 + Cc * 4 * 4
+    out["conv1d_prefill_config2"] = {"tokens": sum(lens), "padded_T": Tm,
+                                     "us": round(t * 1e6, 1),
+                                     "gbs": round(cbytes / t / 1e9, 1),
+                                     "hbm_frac": round(cbytes / t / 1e9 / HBM_PEAK_GBS, 4)}
+    del cpool, cx, cout
     out["prefill_tick"] = prefill_case([256] * 4)
 
     # conv1d decode, config 3 shape

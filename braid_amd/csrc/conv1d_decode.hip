@@ -1,13 +1,24 @@
-// Batched slotted causal depthwise conv1d, one decode step, SiLU fused.
+// Batched slotted causal depthwise conv1d with SiLU: one decode step
+// (conv1d_decode) and a whole chunk of T tokens (conv1d_prefill).
 //
-// Reference behaviour: braid/kernels/csrc/conv1d_decode.cu:40-75. Per channel
-// c of batch row b, with the window st = conv_pool[slot_idx[b], c, 0..K) holding
-// the last K pre-conv inputs (oldest first, K contiguous per channel):
+// Decode reference behaviour: braid/kernels/csrc/conv1d_decode.cu:40-75. Per
+// channel c of batch row b, with the window st = conv_pool[slot_idx[b], c,
+// 0..K) holding the last K pre-conv inputs (oldest first, K contiguous per
+// channel):
 //   w   = (st[1], ..., st[K-1], x[b, c])     window slides left, new value last
 //   st <- w
 //   out[b, c] = SiLU(sum_i w[i] * weight[c, i] + bias[c])
 // SiLU applies to every channel (Q, K and V alike); bias is added after the dot
 // and before the activation.
+//
+// The prefill is the same step applied to tokens 0..len_b-1 of row b with the
+// window held in registers (one pool read and one pool write per chunk). It
+// replaces the reference's prefill conv, torch F.conv1d over [window | x] plus
+// a gather to save the last K real inputs of a ragged row
+// (braid/model/gdn.py:171-226). Its contract is exact: the outputs and the
+// saved window equal conv1d_decode applied token by token, bit for bit,
+// because both run conv_step below. Pad positions (t >= len_b) write 0 and do
+// not move the window.
 //
 // One thread per channel. At K = 4 a channel's window is one 16-byte fp32
 // vector, so the pool read, the pool write and the weight read are single
@@ -26,6 +37,55 @@ __device__ __forceinline__ float conv_widen(uint16_t bf16) {
 
 __device__ __forceinline__ float silu(float a) { return a / (1.f + expf(-a)); }
 
+// Loads a channel's window and weight row (vector accesses at K = 4).
+template <int K>
+__device__ __forceinline__ void load_window(const float* st, const float* wr, float (&w)[K],
+                                            float (&wt)[K]) {
+  if constexpr (K == 4) {
+    const f32x4 s4 = *reinterpret_cast<const f32x4*>(st);
+    const f32x4 w4 = *reinterpret_cast<const f32x4*>(wr);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      w[i] = s4[i];
+      wt[i] = w4[i];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+      w[i] = st[i];
+      wt[i] = wr[i];
+    }
+  }
+}
+
+template <int K>
+__device__ __forceinline__ void store_window(float* st, const float (&w)[K]) {
+  if constexpr (K == 4) {
+    f32x4 s4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s4[i] = w[i];
+    *reinterpret_cast<f32x4*>(st) = s4;
+  } else {
+#pragma unroll
+    for (int i = 0; i < K; ++i) st[i] = w[i];
+  }
+}
+
+// One token: slide the window, append x, dot with the weight row (in window
+// order, as fmas), add the bias, SiLU.
+template <int K>
+__device__ __forceinline__ float conv_step(float (&w)[K], float x, const float (&wt)[K],
+                                           const float* __restrict__ bias, int c) {
+#pragma unroll
+  for (int i = 0; i < K - 1; ++i) w[i] = w[i + 1];
+  w[K - 1] = x;
+  float acc = w[0] * wt[0];
+#pragma unroll
+  for (int i = 1; i < K; ++i) acc = fmaf(w[i], wt[i], acc);
+  if (bias != nullptr) acc += bias[c];
+  return silu(acc);
+}
+
 template <int K, class XT>
 __global__ void __launch_bounds__(256)
 conv1d_decode_kernel(float* __restrict__ conv_pool, const int* __restrict__ slot_idx,
@@ -36,40 +96,44 @@ conv1d_decode_kernel(float* __restrict__ conv_pool, const int* __restrict__ slot
   const int b = blockIdx.y;
   const int slot = slot_idx[b];
   float* st = conv_pool + ((size_t)slot * C + c) * K;
-  const float* wr = weight + (size_t)c * K;
-
   float w[K], wt[K];
-  if constexpr (K == 4) {
-    const f32x4 s4 = *reinterpret_cast<const f32x4*>(st);
-    const f32x4 w4 = *reinterpret_cast<const f32x4*>(wr);
-    w[0] = s4[1];
-    w[1] = s4[2];
-    w[2] = s4[3];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) wt[i] = w4[i];
-  } else {
-#pragma unroll
-    for (int i = 0; i < K - 1; ++i) w[i] = st[i + 1];
-#pragma unroll
-    for (int i = 0; i < K; ++i) wt[i] = wr[i];
-  }
-  w[K - 1] = conv_widen(x[(size_t)b * C + c]);
+  load_window<K>(st, weight + (size_t)c * K, w, wt);
+  const float o = conv_step<K>(w, conv_widen(x[(size_t)b * C + c]), wt, bias, c);
+  store_window<K>(st, w);
+  out[(size_t)b * C + c] = o;
+}
 
-  float acc = w[0] * wt[0];
+// T tokens per launch; the inputs of kUnroll tokens are loaded together ahead
+// of their serial steps.
+template <int K, class XT>
+__global__ void __launch_bounds__(256)
+conv1d_prefill_kernel(float* __restrict__ conv_pool, const int* __restrict__ slot_idx,
+                      const XT* __restrict__ x, const float* __restrict__ weight,
+                      const float* __restrict__ bias, float* __restrict__ out, int C, int T,
+                      const int* __restrict__ seq_lens) {
+  constexpr int kUnroll = 8;
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= C) return;
+  const int b = blockIdx.y;
+  const int slot = slot_idx[b];
+  int len = T;
+  if (seq_lens != nullptr) len = min(max(seq_lens[b], 0), T);
+  float* st = conv_pool + ((size_t)slot * C + c) * K;
+  float w[K], wt[K];
+  load_window<K>(st, weight + (size_t)c * K, w, wt);
+  const XT* xb = x + (size_t)b * T * C + c;
+  float* ob = out + (size_t)b * T * C + c;
+  int t = 0;
+  for (; t + kUnroll <= len; t += kUnroll) {
+    float xs[kUnroll];
 #pragma unroll
-  for (int i = 1; i < K; ++i) acc = fmaf(w[i], wt[i], acc);
-  if (bias != nullptr) acc += bias[c];
-
-  if constexpr (K == 4) {
-    f32x4 s4;
+    for (int u = 0; u < kUnroll; ++u) xs[u] = conv_widen(xb[(size_t)(t + u) * C]);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) s4[i] = w[i];
-    *reinterpret_cast<f32x4*>(st) = s4;
-  } else {
-#pragma unroll
-    for (int i = 0; i < K; ++i) st[i] = w[i];
+    for (int u = 0; u < kUnroll; ++u) ob[(size_t)(t + u) * C] = conv_step<K>(w, xs[u], wt, bias, c);
   }
-  out[(size_t)b * C + c] = silu(acc);
+  for (; t < len; ++t) ob[(size_t)t * C] = conv_step<K>(w, conv_widen(xb[(size_t)t * C]), wt, bias, c);
+  for (; t < T; ++t) ob[(size_t)t * C] = 0.f;
+  store_window<K>(st, w);
 }
 
 template <class XT>
@@ -99,16 +163,28 @@ int launch(int K, float* conv_pool, const int32_t* slot_idx, int B, const XT* x,
   return st != BRAID_OK ? st : ok();
 }
 
-}  // namespace
-}  // namespace braid
+template <class XT>
+int launch_prefill(int K, float* conv_pool, const int32_t* slot_idx, int B, int T, const XT* x,
+                   const float* weight, const float* bias, float* out, int C,
+                   const int32_t* seq_lens, hipStream_t stream) {
+  const int threads = 256;
+  const dim3 grid((unsigned)((C + threads - 1) / threads), (unsigned)B);
+#define BRAID_CONV_PREFILL(KK)                                                               \
+  conv1d_prefill_kernel<KK, XT><<<grid, threads, 0, stream>>>(conv_pool, slot_idx, x, weight, \
+                                                              bias, out, C, T, seq_lens)
+  switch (K) {
+    case 2: BRAID_CONV_PREFILL(2); break;
+    case 3: BRAID_CONV_PREFILL(3); break;
+    case 4: BRAID_CONV_PREFILL(4); break;
+    default: BRAID_CONV_PREFILL(8); break;
+  }
+#undef BRAID_CONV_PREFILL
+  const int st = hip_status(hipGetLastError(), "launching conv1d_prefill_kernel");
+  return st != BRAID_OK ? st : ok();
+}
 
-using namespace braid;
-
-extern "C" int braid_conv1d_decode(float* conv_pool, int64_t n_slots, int C, int K,
-                                   const int32_t* slot_idx, int B, const void* x, int x_dtype,
-                                   const float* weight, const float* bias, float* out,
-                                   void* stream_) {
-  hipStream_t stream = static_cast<hipStream_t>(stream_);
+int check_conv(float* conv_pool, int64_t n_slots, int C, int K, const int32_t* slot_idx, int B,
+               const void* x, int x_dtype, const float* weight, float* out) {
   if (K != 2 && K != 3 && K != 4 && K != 8)
     return fail(BRAID_EINVAL,
                 "conv_kernel " + std::to_string(K) + " is not instantiated (have 2, 3, 4, 8)");
@@ -116,12 +192,48 @@ extern "C" int braid_conv1d_decode(float* conv_pool, int64_t n_slots, int C, int
     return fail(BRAID_EINVAL, "x must be fp32 or bf16 (the activation dtypes braid runs)");
   if (C <= 0 || B < 0 || n_slots <= 0)
     return fail(BRAID_EINVAL, "conv_pool must be [S_max, C, K] with S_max, C > 0");
-  if (B == 0) return ok();
+  if (B == 0) return BRAID_OK;
   if (conv_pool == nullptr || slot_idx == nullptr || x == nullptr || weight == nullptr ||
       out == nullptr)
     return fail(BRAID_EINVAL, "conv_pool/slot_idx/x/weight/out must be non-null");
   if (K == 4 && (!aligned16(conv_pool) || !aligned16(weight)))
     return fail(BRAID_EINVAL, "conv_pool and weight must be 16-byte aligned at K = 4");
+  return BRAID_OK;
+}
+
+}  // namespace
+}  // namespace braid
+
+using namespace braid;
+
+extern "C" int braid_conv1d_prefill(float* conv_pool, int64_t n_slots, int C, int K,
+                                    const int32_t* slot_idx, int B, int T, const void* x,
+                                    int x_dtype, const float* weight, const float* bias,
+                                    float* out, const int32_t* seq_lens, void* stream_) {
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  if (T < 0) return fail(BRAID_EINVAL, "T must be non-negative");
+  const int st0 = check_conv(conv_pool, n_slots, C, K, slot_idx, B, x, x_dtype, weight, out);
+  if (st0 != BRAID_OK) return st0;
+  if (B == 0) return ok();
+  // Rows update their slot's window over the whole chunk: two rows on one slot
+  // would race, so (unlike the one-step decode) slots must be distinct.
+  const int st = validate_slots(slot_idx, B, n_slots, true, stream);
+  if (st != BRAID_OK) return st;
+  if (x_dtype == BRAID_F32)
+    return launch_prefill(K, conv_pool, slot_idx, B, T, static_cast<const float*>(x), weight,
+                          bias, out, C, seq_lens, stream);
+  return launch_prefill(K, conv_pool, slot_idx, B, T, static_cast<const uint16_t*>(x), weight,
+                        bias, out, C, seq_lens, stream);
+}
+
+extern "C" int braid_conv1d_decode(float* conv_pool, int64_t n_slots, int C, int K,
+                                   const int32_t* slot_idx, int B, const void* x, int x_dtype,
+                                   const float* weight, const float* bias, float* out,
+                                   void* stream_) {
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  const int st0 = check_conv(conv_pool, n_slots, C, K, slot_idx, B, x, x_dtype, weight, out);
+  if (st0 != BRAID_OK) return st0;
+  if (B == 0) return ok();
   const int st = validate_slots(slot_idx, B, n_slots, false, stream);
   if (st != BRAID_OK) return st;
   if (x_dtype == BRAID_F32)

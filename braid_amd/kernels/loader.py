@@ -56,6 +56,8 @@ SIGNATURES = {
                                _vp], _i32),
     "braid_conv1d_decode": ([_vp, _i64, _i32, _i32, _vp, _i32, _vp, _i32, _vp, _vp,
                              _vp, _vp], _i32),
+    "braid_conv1d_prefill": ([_vp, _i64, _i32, _i32, _vp, _i32, _i32, _vp, _i32, _vp, _vp,
+                              _vp, _vp, _vp], _i32),
     "braid_quantize_act_workspace": ([_i64], _i32),
     "braid_quantize_act": ([_vp, _i32, _i64, _vp, _vp, _vp, _vp], _i32),
 }
@@ -269,6 +271,42 @@ class GDNKernels:
         self._call("braid_conv1d_decode", conv_pool.device, _ptr(conv_pool), n_slots, C, K,
                    _ptr(slot_idx), B, _ptr(x), _ACT_DTYPES[x.dtype], _ptr(weight), bias_p,
                    _ptr(out))
+
+    def conv1d_prefill(self, conv_pool, slot_idx, x, weight, bias, out,
+                       seq_lens: Optional[torch.Tensor] = None) -> None:
+        """Chunked causal conv1d + SiLU over x [B, T, C] (replaces the torch
+        F.conv1d prefill of braid/model/gdn.py:171-226). Equals conv1d_decode
+        applied to each live token, bit for bit; pad positions write 0."""
+        _check(conv_pool.is_cuda and conv_pool.dtype == torch.float32,
+               "conv_pool must be cuda fp32")
+        _check(conv_pool.is_contiguous(), "conv_pool must be contiguous")
+        _check(slot_idx.dtype == torch.int32, "slot_idx must be int32")
+        _check(slot_idx.is_cuda and slot_idx.is_contiguous(), "slot_idx must be contiguous cuda")
+        _check(conv_pool.dim() == 3, "conv_pool must be [S_max, C, K]")
+        n_slots, C, K = conv_pool.shape
+        _check(x.dim() == 3 and x.size(2) == C, "x must be [B, T, C]")
+        B, T = x.size(0), x.size(1)
+        _check(tuple(out.shape) == (B, T, C), "out must be [B, T, C]")
+        _check(tuple(weight.shape) == (C, K), "weight must be [C, K]")
+        _check_dense_f32((weight,), "weight must be contiguous cuda fp32")
+        _check(slot_idx.numel() == B, "slot_idx must have one entry per batch row")
+        _check(x.dtype in _ACT_DTYPES,
+               "x must be fp32 or bf16 (the activation dtypes braid runs)")
+        _check(x.is_cuda and x.is_contiguous(), "x must be contiguous")
+        _check(out.is_cuda and out.dtype == torch.float32 and out.is_contiguous(),
+               "out must be contiguous fp32")
+        bias_p = None
+        if bias is not None and bias.numel() > 0:
+            _check_dense_f32((bias,), "bias must be contiguous cuda fp32")
+            _check(bias.numel() == C, "bias must be [C]")
+            bias_p = _ptr(bias)
+        if seq_lens is not None:
+            _check(seq_lens.is_cuda and seq_lens.dtype == torch.int32
+                   and seq_lens.is_contiguous(), "seq_lens must be contiguous cuda int32")
+            _check(seq_lens.numel() == B, "seq_lens must have one entry per batch row")
+        self._call("braid_conv1d_prefill", conv_pool.device, _ptr(conv_pool), n_slots, C, K,
+                   _ptr(slot_idx), B, T, _ptr(x), _ACT_DTYPES[x.dtype], _ptr(weight), bias_p,
+                   _ptr(out), _ptr(seq_lens))
 
     # -- FP8 activation quant ---------------------------------------------------
 

@@ -134,6 +134,27 @@ int braid_conv1d_decode(float* conv_pool, int64_t n_slots, int C, int K,
                         float* out, void* stream);
 
 /*
+ * Chunked causal conv1d (prefill), SiLU fused: T tokens per launch.
+ * Replaces the reference's prefill conv, which is torch code rather than a
+ * kernel: F.conv1d over [cached window | x] plus a gather that saves the last
+ * K real inputs of each ragged row (braid/model/gdn.py:171-226).
+ *
+ *   conv_pool [n_slots, C, K] fp32, as for braid_conv1d_decode
+ *   x         [B, T, C] of x_dtype (BRAID_F32 or BRAID_BF16), dense
+ *   out       [B, T, C] fp32
+ *   seq_lens  [B] int32 device, or NULL (all T tokens live). Row b runs tokens
+ *             0..min(seq_lens[b], T)-1; 0 and values > T are legal.
+ * For live tokens the outputs and the window left in the pool equal
+ * braid_conv1d_decode applied token by token, bit for bit. Pad positions
+ * (t >= len) are written as 0 and do not move the window. Slots must be
+ * distinct (each row rewrites its window).
+ */
+int braid_conv1d_prefill(float* conv_pool, int64_t n_slots, int C, int K,
+                         const int32_t* slot_idx, int B, int T, const void* x,
+                         int x_dtype, const float* weight, const float* bias,
+                         float* out, const int32_t* seq_lens, void* stream);
+
+/*
  * Number of fp32 partials braid_quantize_act needs as workspace for an
  * n-element activation.
  */

@@ -195,6 +195,21 @@ def conv1d_decode(conv_pool: np.ndarray, slot_idx, x, weight, bias) -> np.ndarra
     return out
 
 
+def conv1d_prefill(conv_pool: np.ndarray, slot_idx, x, weight, bias, seq_lens=None):
+    """T tokens of the decode step per row: x [B, T, C] fp32; row b runs tokens
+    0..min(seq_lens[b], T)-1 (all T when seq_lens is None); pad outputs are 0
+    and leave the window alone. Returns out [B, T, C]."""
+    x = _c(x)
+    B, T, C = x.shape
+    out = np.zeros((B, T, C), dtype=np.float32)
+    idx = np.asarray(slot_idx, dtype=np.int64)
+    for b in range(B):
+        n = T if seq_lens is None else int(min(max(int(seq_lens[b]), 0), T))
+        for t in range(n):
+            out[b, t] = conv1d_decode(conv_pool, idx[b:b + 1], x[b:b + 1, t], weight, bias)[0]
+    return out
+
+
 # ---- FP8 ---------------------------------------------------------------------
 
 def quantize_act(x: np.ndarray):

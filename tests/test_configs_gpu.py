@@ -3,8 +3,9 @@ properties plus sampled-row oracle parity.
 
   config 1  batched decode B=128, 160-slot fp16 pool, random permutation of
             128 distinct slots, 64 consecutive steps
-  config 2  ragged prefill, 8 sequences of U[64, 1024] tokens, causal conv
-            first; final states equal the decode kernel applied T_b times
+  config 2  ragged prefill, 8 sequences of U[64, 1024] tokens: native conv
+            prefill + raw-gate chunk scan, bit-identical to conv1d_decode +
+            gdn_decode_raw applied T_b times
   config 3  24 GDN layers of quant -> conv1d decode -> gated decode at B=64
   config 4  a mixed tick: 96 decode rows + 4 x 256-token prefill chunks on
             fresh slots of one 192-slot fp16 pool, eager and graph-captured
@@ -14,7 +15,6 @@ from __future__ import annotations
 import numpy as np
 import pytest
 import torch
-import torch.nn.functional as F
 
 import oracle
 from gpu_helpers import ATOL, DEV, RTOL, act_np, gen, to_np_pool, ulp16
@@ -79,46 +79,52 @@ def test_config1_batched_decode_b128_fp16_pool_64_steps(kern):
     assert torch.isfinite(pool.float()).all()
 
 
-def _causal_conv(x, w, bias):
-    """Depthwise causal conv + SiLU over [B, T, C] from a zero window (fresh
-    sequences), as braid/model/gdn.py:221-227 spells it with F.conv1d."""
-    T = x.shape[1]
-    out = F.conv1d(x.transpose(1, 2), w.unsqueeze(1), bias, padding=w.shape[1] - 1,
-                   groups=x.shape[2])
-    return F.silu(out[:, :, :T]).transpose(1, 2).contiguous()
-
-
 def test_config2_ragged_prefill_equals_decode_t_times(kern):
+    """Config 2 end to end on the native kernels: causal conv prefill (fp16
+    weights widened to fp32, SiLU) then the raw-gate chunk scan with seq_lens,
+    against the decode path — conv1d_decode then gdn_decode_raw on strided
+    q/k/v views — applied token by token. Conv windows, states and every live
+    output must be bit-identical."""
     B = 8
     lens = torch.randint(64, 1025, (B,), generator=torch.Generator().manual_seed(2))
     T = int(lens.max())
     g = gen(3)
     w = (torch.randn(C, 4, generator=g, device=DEV) * 0.1).half().float()
-    x = torch.randn(B, T, C, generator=g, device=DEV)
-    qkv = _causal_conv(x, w, None)
-    q = qkv[..., : G * D].reshape(B, T, G, D).contiguous()
-    k = qkv[..., G * D: 2 * G * D].reshape(B, T, G, D).contiguous()
-    v = qkv[..., 2 * G * D:].reshape(B, T, H, D).contiguous()
+    x = torch.randn(B, T, C, generator=g, device=DEV).to(torch.bfloat16)
     a_raw = torch.randn(B, T, H, generator=g, device=DEV)
     b_raw = torch.randn(B, T, H, generator=g, device=DEV)
     A, dtb = gate_consts(4)
     pool0 = (torch.randn(12, H, D, D, generator=g, device=DEV) * 0.02).half()
+    conv0 = torch.zeros(12, C, 4, device=DEV)
     slots = torch.tensor([11, 3, 7, 0, 5, 9, 2, 6], dtype=torch.int32, device=DEV)
     seq = lens.to(torch.int32).to(DEV)
 
-    pc = pool0.clone()
+    # prefill path
+    pc, cc = pool0.clone(), conv0.clone()
+    qkv = torch.empty(B, T, C, device=DEV)
+    kern.conv1d_prefill(cc, slots, x, w, None, qkv, seq)
+    q = qkv[..., : G * D].reshape(B, T, G, D).contiguous()
+    k = qkv[..., G * D: 2 * G * D].reshape(B, T, G, D).contiguous()
+    v = qkv[..., 2 * G * D:].reshape(B, T, H, D).contiguous()
     yc = torch.empty(B, T, H, D, device=DEV)
     kern.gdn_prefill_raw(pc, slots, q, k, v, a_raw, b_raw, A, dtb, yc, seq)
 
-    ps = pool0.clone()
+    # decode path, one token at a time
+    ps, cs = pool0.clone(), conv0.clone()
     lens_l = lens.tolist()
     for t in range(T):
         live = [b for b in range(B) if t < lens_l[b]]
+        sl = slots[live].contiguous()
+        co = torch.empty(len(live), C, device=DEV)
+        kern.conv1d_decode(cs, sl, x[live, t].contiguous(), w, None, co)
+        qd, kd, vd = torch.split(co, [G * D, G * D, H * D], dim=-1)
         ys = torch.empty(len(live), H, D, device=DEV)
-        kern.gdn_decode_raw(ps, slots[live].contiguous(), q[live, t].contiguous(),
-                            k[live, t].contiguous(), v[live, t].contiguous(),
-                            a_raw[live, t].contiguous(), b_raw[live, t].contiguous(), A, dtb, ys)
-        assert torch.equal(ys, yc[live, t]), f"token {t}: outputs differ"
+        kern.gdn_decode_raw(ps, sl, qd.unflatten(-1, (G, D)), kd.unflatten(-1, (G, D)),
+                            vd.unflatten(-1, (H, D)), a_raw[live, t].contiguous(),
+                            b_raw[live, t].contiguous(), A, dtb, ys)
+        assert torch.equal(co, qkv[live, t]), f"token {t}: conv outputs differ"
+        assert torch.equal(ys, yc[live, t]), f"token {t}: scan outputs differ"
+    assert torch.equal(cc, cs), "conv windows differ from decode applied T_b times"
     assert torch.equal(pc, ps), "final states differ from decode applied T_b times"
     untouched = [1, 4, 8, 10]
     assert torch.equal(pc[untouched], pool0[untouched])

@@ -145,3 +145,71 @@ def test_graph_replay_survives_slot_reassignment(kern):
         torch.cuda.synchronize()
         np.testing.assert_allclose(out.cpu().numpy(), out_ref, rtol=RTOL, atol=ATOL)
         np.testing.assert_array_equal(p.cpu().numpy(), ref_pool)
+
+
+# --- chunked prefill conv ----------------------------------------------------------
+
+def _prefill_inputs(B, T, C, K, dt, seed):
+    g = gen(seed)
+    pool0 = torch.randn(B + 3, C, K, generator=g, device=DEV) * 0.5
+    x = torch.randn(B, T, C, generator=g, device=DEV).to(dt)
+    w = torch.randn(C, K, generator=g, device=DEV) * 0.3
+    bias = torch.randn(C, generator=g, device=DEV) * 0.1
+    return pool0, x, w, bias
+
+
+@pytest.mark.parametrize("K", [2, 3, 4, 8])
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16], ids=["f32-x", "bf16-x"])
+def test_prefill_equals_decode_token_by_token(kern, K, dt):
+    B, T, C = 4, 21, 512
+    pool0, x, w, bias = _prefill_inputs(B, T, C, K, dt, seed=K)
+    slots = torch.tensor([5, 0, 3, 1], dtype=torch.int32, device=DEV)
+    lens = torch.tensor([21, 0, 9, 40], dtype=torch.int32, device=DEV)  # full, empty, ragged, > T
+    pp = pool0.clone()
+    out = torch.full((B, T, C), float("nan"), device=DEV)
+    kern.conv1d_prefill(pp, slots, x, w, bias, out, lens)
+    pd = pool0.clone()
+    lens_l = [min(max(int(n), 0), T) for n in lens.tolist()]
+    for t in range(T):
+        live = [b for b in range(B) if t < lens_l[b]]
+        if not live:
+            continue
+        o = torch.empty(len(live), C, device=DEV)
+        kern.conv1d_decode(pd, slots[live].contiguous(), x[live, t].contiguous(), w, bias, o)
+        assert torch.equal(o, out[live, t]), f"token {t} differs from decode"
+    assert torch.equal(pp, pd), "saved windows differ from decode applied per token"
+    for b in range(B):
+        assert (out[b, lens_l[b]:] == 0).all(), "pad positions must be written as 0"
+
+
+def test_prefill_matches_oracle_and_saves_the_last_k_real_inputs(kern):
+    B, T, C, K = 3, 17, 256, 4
+    pool0, x, w, bias = _prefill_inputs(B, T, C, K, torch.bfloat16, seed=7)
+    slots = torch.tensor([2, 4, 0], dtype=torch.int32, device=DEV)
+    lens = torch.tensor([17, 5, 2], dtype=torch.int32, device=DEV)
+    ref_pool = pool0.cpu().numpy().copy()
+    out_ref = oracle.conv1d_prefill(ref_pool, slots.cpu().numpy(), x.float().cpu().numpy(),
+                                    w.cpu().numpy(), bias.cpu().numpy(), lens.cpu().numpy())
+    p = pool0.clone()
+    out = torch.empty(B, T, C, device=DEV)
+    kern.conv1d_prefill(p, slots, x, w, bias, out, lens)
+    np.testing.assert_allclose(out.cpu().numpy(), out_ref, rtol=RTOL, atol=ATOL)
+    np.testing.assert_array_equal(p.cpu().numpy(), ref_pool)
+    # the saved window of a ragged row is its last K real inputs (here len 5)
+    np.testing.assert_array_equal(p[4].cpu().numpy(), x[1, 1:5].float().t().cpu().numpy())
+
+
+def test_prefill_rejects_duplicate_slots_and_handles_no_seq_lens(kern):
+    B, T, C, K = 2, 5, 256, 4
+    pool0, x, w, bias = _prefill_inputs(B, T, C, K, torch.float32, seed=9)
+    out = torch.empty(B, T, C, device=DEV)
+    with pytest.raises(RuntimeError, match="duplicate|distinct"):
+        kern.conv1d_prefill(pool0.clone(), torch.tensor([1, 1], dtype=torch.int32, device=DEV),
+                            x, w, bias, out)
+    p1, p2 = pool0.clone(), pool0.clone()
+    o1, o2 = torch.empty_like(out), torch.empty_like(out)
+    slots = torch.tensor([1, 3], dtype=torch.int32, device=DEV)
+    kern.conv1d_prefill(p1, slots, x, w, bias, o1, None)
+    kern.conv1d_prefill(p2, slots, x, w, bias, o2,
+                        torch.full((B,), T, dtype=torch.int32, device=DEV))
+    assert torch.equal(o1, o2) and torch.equal(p1, p2)

@@ -307,3 +307,31 @@ def test_state_bytes_match_reference_measurement():
     """63.75 MiB of recurrent state per sequence (reference test_gdn_ref.py:24-34)."""
     cfg = GDNConfig.qwen36_35b_a3b()
     assert abs(cfg.recurrent_bytes_per_seq / 2 ** 20 - 63.75) < 0.1
+
+
+def test_conv_prefill_matches_the_reference_torch_spelling():
+    """oracle.conv1d_prefill against the reference's own prefill conv, restated
+    in torch on the CPU from braid/model/gdn.py:193-222: F.conv1d over
+    [cached window | x] with no padding, the last T outputs, and the window
+    saved by gathering joined[len : len + K] for a ragged row."""
+    rng = np.random.default_rng(14)
+    B, T, C, K = 3, 9, 32, 4
+    pool = rng.standard_normal((5, C, K)).astype(np.float32)
+    x = rng.standard_normal((B, T, C)).astype(np.float32)
+    w = rng.standard_normal((C, K)).astype(np.float32)
+    bias = rng.standard_normal(C).astype(np.float32)
+    slots = np.array([3, 0, 4])
+    lens = np.array([9, 4, 1])
+    tp = torch.from_numpy(pool.copy())
+    window = tp[torch.from_numpy(slots)]                                  # [B, C, K]
+    joined = torch.cat([window, torch.from_numpy(x).transpose(1, 2)], -1)  # [B, C, K+T]
+    idx = torch.from_numpy(lens)[:, None] + torch.arange(K)[None]
+    keep = joined.gather(2, idx[:, None].expand(B, C, K))
+    ref_out = F.silu(F.conv1d(joined, torch.from_numpy(w)[:, None, :], torch.from_numpy(bias),
+                              padding=0, groups=C)[:, :, -T:]).transpose(1, 2).numpy()
+    got_pool = pool.copy()
+    out = oracle.conv1d_prefill(got_pool, slots, x, w, bias, lens)
+    for b in range(B):
+        np.testing.assert_allclose(out[b, :lens[b]], ref_out[b, :lens[b]], rtol=1e-5, atol=1e-6)
+        assert (out[b, lens[b]:] == 0).all()
+        np.testing.assert_array_equal(got_pool[slots[b]], keep[b].numpy())
