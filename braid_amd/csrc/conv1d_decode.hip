@@ -11,8 +11,8 @@
 // SiLU applies to every channel (Q, K and V alike); bias is added after the dot
 // and before the activation.
 //
-// The prefill is the same step applied to tokens 0..len_b-1 of row b with the
-// window held in registers (one pool read and one pool write per chunk). It
+// The prefill is the same step applied to tokens 0..len_b-1 of row b, with the
+// token axis split into chunks across threads (see conv1d_prefill_kernel). It
 // replaces the reference's prefill conv, torch F.conv1d over [window | x] plus
 // a gather to save the last K real inputs of a ragged row
 // (braid/model/gdn.py:171-226). Its contract is exact: the outputs and the
@@ -55,6 +55,18 @@ __device__ __forceinline__ void load_window(const float* st, const float* wr, fl
       w[i] = st[i];
       wt[i] = wr[i];
     }
+  }
+}
+
+template <int K>
+__device__ __forceinline__ void load_weights(const float* wr, float (&wt)[K]) {
+  if constexpr (K == 4) {
+    const f32x4 w4 = *reinterpret_cast<const f32x4*>(wr);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) wt[i] = w4[i];
+  } else {
+#pragma unroll
+    for (int i = 0; i < K; ++i) wt[i] = wr[i];
   }
 }
 
@@ -103,37 +115,129 @@ conv1d_decode_kernel(float* __restrict__ conv_pool, const int* __restrict__ slot
   out[(size_t)b * C + c] = o;
 }
 
-// T tokens per launch; the inputs of kUnroll tokens are loaded together ahead
-// of their serial steps.
-template <int K, class XT>
+// Loads NC consecutive channels' values of one token (NC = 1 or 4; 4 is a
+// single 8-byte bf16 or 16-byte fp32 vector).
+template <int NC>
+__device__ __forceinline__ void load_x(const float* p, float (&o)[NC]) {
+  if constexpr (NC == 4) {
+    const f32x4 v = *reinterpret_cast<const f32x4*>(p);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[j] = v[j];
+  } else {
+    o[0] = *p;
+  }
+}
+template <int NC>
+__device__ __forceinline__ void load_x(const uint16_t* p, float (&o)[NC]) {
+  if constexpr (NC == 4) {
+    const uint2 v = *reinterpret_cast<const uint2*>(p);
+    o[0] = conv_widen((uint16_t)(v.x & 0xffffu));
+    o[1] = conv_widen((uint16_t)(v.x >> 16));
+    o[2] = conv_widen((uint16_t)(v.y & 0xffffu));
+    o[3] = conv_widen((uint16_t)(v.y >> 16));
+  } else {
+    o[0] = conv_widen(*p);
+  }
+}
+template <int NC>
+__device__ __forceinline__ void store_out(float* p, const float (&o)[NC]) {
+  if constexpr (NC == 4) {
+    *reinterpret_cast<f32x4*>(p) = (f32x4){o[0], o[1], o[2], o[3]};
+  } else {
+    *p = o[0];
+  }
+}
+
+// T tokens per launch. A conv output depends only on the K most recent
+// inputs, not on earlier outputs, so the token axis is cut into chunks of
+// kChunk tokens and each thread runs NC adjacent channels over one chunk
+// (NC = 4 gives 8- or 16-byte loads and 16-byte stores): a thread starts from
+// the K - 1 inputs before its chunk (from the cached window for the first
+// chunk, from x otherwise) and runs conv_step over its tokens — the same
+// window values in the same order as the token-by-token decode, so the same
+// bits. Only the first chunk's thread touches the pool: it reads the old window
+// and afterwards writes the new one (the last K inputs of the row's live
+// tokens, spliced after the old window when fewer than K), so no thread of
+// another chunk can see it half-updated.
+template <int K, int NC, class XT>
 __global__ void __launch_bounds__(256)
 conv1d_prefill_kernel(float* __restrict__ conv_pool, const int* __restrict__ slot_idx,
                       const XT* __restrict__ x, const float* __restrict__ weight,
                       const float* __restrict__ bias, float* __restrict__ out, int C, int T,
                       const int* __restrict__ seq_lens) {
-  constexpr int kUnroll = 8;
-  const int c = blockIdx.x * blockDim.x + threadIdx.x;
-  if (c >= C) return;
-  const int b = blockIdx.y;
-  const int slot = slot_idx[b];
+  constexpr int kChunk = 16;
+  const int c0 = (blockIdx.x * blockDim.x + threadIdx.x) * NC;
+  if (c0 >= C) return;
+  const int b = blockIdx.z;
+  const int t0 = blockIdx.y * kChunk;
   int len = T;
   if (seq_lens != nullptr) len = min(max(seq_lens[b], 0), T);
-  float* st = conv_pool + ((size_t)slot * C + c) * K;
-  float w[K], wt[K];
-  load_window<K>(st, weight + (size_t)c * K, w, wt);
-  const XT* xb = x + (size_t)b * T * C + c;
-  float* ob = out + (size_t)b * T * C + c;
-  int t = 0;
-  for (; t + kUnroll <= len; t += kUnroll) {
-    float xs[kUnroll];
+  const XT* xb = x + (size_t)b * T * C + c0;
+  float* ob = out + (size_t)b * T * C + c0;
+  float* st = conv_pool + ((size_t)slot_idx[b] * C + c0) * K;
+
+  float w[NC][K], wt[NC][K], old[NC][K];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) xs[u] = conv_widen(xb[(size_t)(t + u) * C]);
+  for (int j = 0; j < NC; ++j) {
+    if (t0 == 0) {
+      load_window<K>(st + j * K, weight + (size_t)(c0 + j) * K, old[j], wt[j]);
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) ob[(size_t)(t + u) * C] = conv_step<K>(w, xs[u], wt, bias, c);
+      for (int i = 0; i < K; ++i) w[j][i] = old[j][i];
+    } else {
+      load_weights<K>(weight + (size_t)(c0 + j) * K, wt[j]);
+    }
   }
-  for (; t < len; ++t) ob[(size_t)t * C] = conv_step<K>(w, conv_widen(xb[(size_t)t * C]), wt, bias, c);
-  for (; t < T; ++t) ob[(size_t)t * C] = 0.f;
-  store_window<K>(st, w);
+  if (t0 != 0) {
+    // inputs t0-K .. t0-1 (t0 >= kChunk >= K, so all come from x); w[.][0] is
+    // shifted out by the first step and never used
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+      float xi[NC];
+      load_x<NC>(xb + (size_t)(t0 - K + i) * C, xi);
+#pragma unroll
+      for (int j = 0; j < NC; ++j) w[j][i] = xi[j];
+    }
+  }
+  const int t1 = min(t0 + kChunk, T);
+  const int live_end = min(t1, len);
+  float xs[kChunk][NC];
+#pragma unroll
+  for (int u = 0; u < kChunk; ++u) {
+    if (t0 + u < live_end) {
+      load_x<NC>(xb + (size_t)(t0 + u) * C, xs[u]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < NC; ++j) xs[u][j] = 0.f;
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kChunk; ++u) {
+    const int t = t0 + u;
+    float o[NC];
+    if (t < live_end) {
+#pragma unroll
+      for (int j = 0; j < NC; ++j) o[j] = conv_step<K>(w[j], xs[u][j], wt[j], bias, c0 + j);
+      store_out<NC>(ob + (size_t)t * C, o);
+    } else if (t < t1) {
+#pragma unroll
+      for (int j = 0; j < NC; ++j) o[j] = 0.f;
+      store_out<NC>(ob + (size_t)t * C, o);
+    }
+  }
+  if (t0 == 0) {
+    // new window = the last K entries of [old window | x_0 .. x_{len-1}]
+    float nw[NC][K];
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+      const int src = len - K + i;  // position in x; negative = from the old window
+      float xi[NC];
+      if (src >= 0) load_x<NC>(xb + (size_t)src * C, xi);
+#pragma unroll
+      for (int j = 0; j < NC; ++j) nw[j][i] = src >= 0 ? xi[j] : old[j][K + src];
+    }
+#pragma unroll
+    for (int j = 0; j < NC; ++j) store_window<K>(st + j * K, nw[j]);
+  }
 }
 
 template <class XT>
@@ -167,17 +271,34 @@ template <class XT>
 int launch_prefill(int K, float* conv_pool, const int32_t* slot_idx, int B, int T, const XT* x,
                    const float* weight, const float* bias, float* out, int C,
                    const int32_t* seq_lens, hipStream_t stream) {
+  if (T == 0) return ok();  // no tokens: nothing to compute, the windows stay as they are
   const int threads = 256;
-  const dim3 grid((unsigned)((C + threads - 1) / threads), (unsigned)B);
-#define BRAID_CONV_PREFILL(KK)                                                               \
-  conv1d_prefill_kernel<KK, XT><<<grid, threads, 0, stream>>>(conv_pool, slot_idx, x, weight, \
-                                                              bias, out, C, T, seq_lens)
-  switch (K) {
-    case 2: BRAID_CONV_PREFILL(2); break;
-    case 3: BRAID_CONV_PREFILL(3); break;
-    case 4: BRAID_CONV_PREFILL(4); break;
-    default: BRAID_CONV_PREFILL(8); break;
+  constexpr int kChunk = 16;
+  // Four channels per thread when every vector access stays aligned: C a
+  // multiple of 4 (then each row and window block is too) and 16-byte bases.
+  const bool vec4 = (C % 4 == 0) && aligned16(x) && aligned16(out) && aligned16(conv_pool) &&
+                    aligned16(weight);
+  const int nc = vec4 ? 4 : 1;
+  const int per_row = (C + nc - 1) / nc;
+  const dim3 grid((unsigned)((per_row + threads - 1) / threads),
+                  (unsigned)((T + kChunk - 1) / kChunk), (unsigned)B);
+#define BRAID_CONV_PREFILL(KK, NC)                                                         \
+  conv1d_prefill_kernel<KK, NC, XT><<<grid, threads, 0, stream>>>(conv_pool, slot_idx, x,  \
+                                                                  weight, bias, out, C, T, \
+                                                                  seq_lens)
+#define BRAID_CONV_PREFILL_K(NC)              \
+  switch (K) {                                \
+    case 2: BRAID_CONV_PREFILL(2, NC); break; \
+    case 3: BRAID_CONV_PREFILL(3, NC); break; \
+    case 4: BRAID_CONV_PREFILL(4, NC); break; \
+    default: BRAID_CONV_PREFILL(8, NC); break; \
   }
+  if (vec4) {
+    BRAID_CONV_PREFILL_K(4)
+  } else {
+    BRAID_CONV_PREFILL_K(1)
+  }
+#undef BRAID_CONV_PREFILL_K
 #undef BRAID_CONV_PREFILL
   const int st = hip_status(hipGetLastError(), "launching conv1d_prefill_kernel");
   return st != BRAID_OK ? st : ok();

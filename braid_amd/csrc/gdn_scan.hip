@@ -1,8 +1,9 @@
 // Batched Gated DeltaNet decode step and chunk prefill scan for gfx950.
 //
-// Both kernels launch one 256-thread workgroup (four waves, 32 state rows
-// each) per (batch row, value head) tile and run the same per-token device
-// function, braid::gdn_token. Decode loads the tile from the slot-indexed pool,
+// Both kernels launch one workgroup per (batch row, value head) tile and run
+// the same per-token device function, braid::gdn_token: decode with four waves
+// of 32 state rows x 128 columns, prefill with eight waves (the same rows,
+// each tile's columns split in two halves), which changes no bit. Decode loads the tile from the slot-indexed pool,
 // runs one token and stores it back; prefill loads it once, runs T tokens with
 // the tile resident in registers (in the pool's storage type) and stores it
 // once. Reference behaviour: braid/kernels/csrc/gdn_decode.cu:156-272 (decode)
@@ -24,18 +25,17 @@ struct Storage<BF16> { using T = uint16_t; };
 
 // One decode token for the tile (blockIdx.x = b * H + h).
 template <class Tag, class Gates>
-__device__ __forceinline__ void decode_tile(typename Storage<Tag>::T* __restrict__ pool,
-                                            const int* __restrict__ slot_idx,
-                                            const float* __restrict__ q,
-                                            const float* __restrict__ k,
-                                            const float* __restrict__ v, const Gates& gates,
-                                            float* __restrict__ y, int H, int heads_per_group,
-                                            long q_row, long k_row, long v_row) {
+__global__ void __launch_bounds__(tile_threads(kDecodeCols))
+gdn_decode_kernel(typename Storage<Tag>::T* __restrict__ pool, const int* __restrict__ slot_idx,
+                  const float* __restrict__ q, const float* __restrict__ k,
+                  const float* __restrict__ v, Gates gates, float* __restrict__ y, int H,
+                  int heads_per_group, long q_row, long k_row, long v_row) {
+  constexpr int CPL = kDecodeCols;
   using ST = typename Storage<Tag>::T;
   const int b = blockIdx.x / H;
   const int h = blockIdx.x - b * H;
   const int g = h / heads_per_group;
-  const LaneMap L(threadIdx.x);
+  const LaneMap<CPL> L(threadIdx.x);
 
   // The slot comes from device memory, so one captured graph serves any slot
   // assignment (gdn_decode.cu:230-236).
@@ -44,66 +44,62 @@ __device__ __forceinline__ void decode_tile(typename Storage<Tag>::T* __restrict
   ST* tile = pool + ((size_t)slot * H + h) * (kSS * kHD) + L.col0;
 
   // Issue the whole tile's loads first; the norms and gates below overlap them.
-  Row8<Tag> S[kRowsPerLane];
+  Row<Tag, CPL> S[kRowsPerLane];
 #pragma unroll
   for (int i = 0; i < kRowsPerLane; ++i) S[i].load_nt(tile + (size_t)L.row(i) * kHD);
 
-  float vv[8];
-  load8(v + (size_t)b * v_row + (size_t)h * kHD + L.col0, vv);
+  float vv[CPL];
+  loadN<CPL>(v + (size_t)b * v_row + (size_t)h * kHD + L.col0, vv);
   QK qk;
-  normalize_qk(L, q + (size_t)b * q_row + (size_t)g * kSS,
-               k + (size_t)b * k_row + (size_t)g * kSS, qk);
+  normalize_qk(L, q + (size_t)b * q_row + (size_t)g * kSS, k + (size_t)b * k_row + (size_t)g * kSS,
+               qk);
   publish_gates(L, gates, gates.load(b, h, 0, H, 1), h, lds);
 
-  float yy[8];
-  gdn_token<Tag>(L, S, qk, vv, lds, yy);
+  float yy[CPL];
+  gdn_token<Tag, CPL>(L, S, qk, vv, lds, yy);
 
 #pragma unroll
   for (int i = 0; i < kRowsPerLane; ++i) S[i].store_nt(tile + (size_t)L.row(i) * kHD);
-  // Each column chunk's totals sit in all its lanes; one lane per chunk writes them.
-  if (stores_y(L)) store8(y + ((size_t)b * H + h) * kHD + L.col0, yy);
+  // Each column's totals sit in all lanes of its chunk; one lane per chunk writes them.
+  if (L.stores_y()) storeN<CPL>(y + ((size_t)b * H + h) * kHD + L.col0, yy);
 }
 
+// T tokens for the tile with the state resident in registers, in the column-
+// split layout (4 columns per lane, eight waves): the same per-column
+// arithmetic as the decode kernel, token by token.
 template <class Tag, class Gates>
-__global__ void __launch_bounds__(kTileThreads)
-gdn_decode_kernel(typename Storage<Tag>::T* __restrict__ pool, const int* __restrict__ slot_idx,
-                  const float* __restrict__ q, const float* __restrict__ k,
-                  const float* __restrict__ v, Gates gates, float* __restrict__ y, int H,
-                  int heads_per_group, long q_row, long k_row, long v_row) {
-  decode_tile<Tag, Gates>(pool, slot_idx, q, k, v, gates, y, H, heads_per_group, q_row, k_row,
-                          v_row);
-}
-
-template <class Tag, class Gates>
-__global__ void __launch_bounds__(kTileThreads)
+__global__ void __launch_bounds__(tile_threads(kPrefillCols))
 gdn_prefill_kernel(typename Storage<Tag>::T* __restrict__ pool,
                    const int* __restrict__ slot_idx,
                    const float* __restrict__ q, const float* __restrict__ k,
                    const float* __restrict__ v, Gates gates, float* __restrict__ y,
                    int H, int G, int heads_per_group, int T) {
+  constexpr int CPL = kPrefillCols;
   using ST = typename Storage<Tag>::T;
   const int b = blockIdx.x / H;
   const int h = blockIdx.x - b * H;
   const int g = h / heads_per_group;
-  const LaneMap L(threadIdx.x);
+  const LaneMap<CPL> L(threadIdx.x);
 
   __shared__ TileLds lds;
   const int slot = slot_idx[b];
   ST* tile = pool + ((size_t)slot * H + h) * (kSS * kHD) + L.col0;
 
-  Row8<Tag> S[kRowsPerLane];
+  Row<Tag, CPL> S[kRowsPerLane];
 #pragma unroll
   for (int i = 0; i < kRowsPerLane; ++i) S[i].load_nt(tile + (size_t)L.row(i) * kHD);
 
-  // Software pipeline: token t + 1's inputs are loaded, its q/k normalised and
-  // its gates computed while token t's recurrence runs; none of them depends
-  // on the state, so the serial chain per token is the recurrence alone.
+  // Software pipeline: token t + 1's inputs are loaded while token t's
+  // recurrence runs, and its q/k norms and gates are evaluated right after;
+  // none of them depends on the state. (Evaluating them between token t's two
+  // barriers instead measured slower: wave 0's gate math then stalls the
+  // other waves at the second barrier.)
   QK qk;
-  float vv[8];
+  float vv[CPL];
   if (T > 0) {
     QKRaw raw;
     load_qk(L, q + ((size_t)b * T * G + g) * kSS, k + ((size_t)b * T * G + g) * kSS, raw);
-    load8(v + ((size_t)b * T * H + h) * kHD + L.col0, vv);
+    loadN<CPL>(v + ((size_t)b * T * H + h) * kHD + L.col0, vv);
     publish_gates(L, gates, gates.load(b, h, 0, H, T), h, lds);
     normalize_qk(raw, qk);
   }
@@ -112,22 +108,22 @@ gdn_prefill_kernel(typename Storage<Tag>::T* __restrict__ pool,
     const bool more = t + 1 < T;
     QKRaw raw_n;
     GateRaw gate_n{};
-    float vv_n[8];
+    float vv_n[CPL];
     if (more) {
       load_qk(L, q + ((bt_idx + 1) * G + g) * kSS, k + ((bt_idx + 1) * G + g) * kSS, raw_n);
-      load8(v + ((bt_idx + 1) * H + h) * kHD + L.col0, vv_n);
+      loadN<CPL>(v + ((bt_idx + 1) * H + h) * kHD + L.col0, vv_n);
       gate_n = gates.load(b, h, t + 1, H, T);
     }
-    float yy[8];
-    gdn_token<Tag>(L, S, qk, vv, lds, yy);
-    if (stores_y(L)) store8(y + (bt_idx * H + h) * kHD + L.col0, yy);
+    float yy[CPL];
+    gdn_token<Tag, CPL>(L, S, qk, vv, lds, yy);
+    if (L.stores_y()) storeN<CPL>(y + (bt_idx * H + h) * kHD + L.col0, yy);
     if (more) {
       // lds.gate was last read before this token's second barrier: safe to
       // overwrite; the next token's first barrier publishes the new values.
       publish_gates(L, gates, gate_n, h, lds);
       normalize_qk(raw_n, qk);
 #pragma unroll
-      for (int c = 0; c < 8; ++c) vv[c] = vv_n[c];
+      for (int c = 0; c < CPL; ++c) vv[c] = vv_n[c];
     }
   }
 
@@ -177,7 +173,7 @@ template <class Gates>
 int launch_decode(void* pool, int pool_dtype, const int32_t* slot_idx, int B, int H, int G,
                   const float* q, int64_t q_row, const float* k, int64_t k_row, const float* v,
                   int64_t v_row, Gates gates, float* y, hipStream_t stream) {
-  const dim3 grid((unsigned)B * (unsigned)H), block(kTileThreads);
+  const dim3 grid((unsigned)B * (unsigned)H), block(tile_threads(kDecodeCols));
   const int hpg = H / G;
   switch (pool_dtype) {
     case BRAID_F32:
@@ -201,7 +197,7 @@ template <class Gates>
 int launch_prefill(void* pool, int pool_dtype, const int32_t* slot_idx, int B, int T, int H,
                    int G, const float* q, const float* k, const float* v, Gates gates,
                    float* y, hipStream_t stream) {
-  const dim3 grid((unsigned)B * (unsigned)H), block(kTileThreads);
+  const dim3 grid((unsigned)B * (unsigned)H), block(tile_threads(kPrefillCols));
   const int hpg = H / G;
   switch (pool_dtype) {
     case BRAID_F32:

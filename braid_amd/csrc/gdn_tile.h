@@ -5,28 +5,35 @@
 // the pool layout [n_slots, H, SS, HD] of braid/model/cache.py:127-128. A row
 // is 256 bytes of an fp16 pool.
 //
-// A tile belongs to one workgroup of kWaves = 4 waves (256 threads): wave w
-// owns the 32 full rows [32w, 32w + 32). Lane l of a wave owns the 8-column
-// chunk c8 = l % 16 of rows 32w + r + 4i (r = l / 16, i = 0..7), so each of a
-// lane's eight state accesses is one 16-byte vector and every wave-wide load
-// or store instruction covers four consecutive rows — 1 KiB contiguous for
-// fp16. Measured on MI355X, this whole-row pattern streams ~18% faster than
-// per-wave column panels, and the state goes through nontemporal loads and
-// stores (it is touched once per step and never re-read by the step).
+// Decode layout (8 columns per lane): a tile belongs to one workgroup of four
+// waves (256 threads); wave w owns the 32 full rows [32w, 32w + 32). Lane l of
+// a wave owns the 8-column chunk cc = l % 16 of rows 32w + r + 4i (r = l / 16,
+// i = 0..7), so each of a lane's eight state accesses is one 16-byte vector and
+// every wave-wide load or store instruction covers four consecutive rows —
+// 1 KiB contiguous for fp16. Measured on MI355X, this whole-row pattern streams
+// ~18% faster than per-wave column panels, and the state goes through
+// nontemporal loads and stores (it is touched once per step and never re-read
+// by the step).
 //
 // Every reduction of the recurrence runs over rows s for a fixed column d, in
 // one fixed order that defines the result's bits:
 //   1. sequentially over a lane's eight rows (an fma chain, i = 0..7);
 //   2. a butterfly over the four row groups r of a wave (lane xor 16, then xor
 //      32): partners add the same two operands, so all lanes agree bitwise;
-//   3. across the four waves through LDS, as the pairwise tree
+//   3. across the four row blocks through LDS, as the pairwise tree
 //      (w0 + w1) + (w2 + w3), evaluated the same way by every lane that needs
 //      the total.
+//
+// Prefill layout (4 columns per lane): the same rows, chains, butterflies and
+// tree, with each tile's columns split across two groups of four waves (512
+// threads). A column's arithmetic does not depend on which lane holds it, so
+// the results are the decode layout's bits, while each wave does half the
+// serial per-token work.
 //
 // The state lives in registers in its STORAGE type. Each token widens it to
 // fp32, runs the recurrence in fp32 and narrows it back, exactly as a decode
 // launch does between its load and its store. The prefill scan therefore
-// executes, token for token, the same instructions on the same values as T
+// executes, token for token, the same operations on the same values as T
 // decode launches: chunked prefill equals decode applied T times, bit for bit,
 // for fp32, fp16 and bf16 pools alike.
 //
@@ -45,33 +52,30 @@
 
 namespace braid {
 
-constexpr int kSS = 128;                          // key dim (state rows)
-constexpr int kHD = 128;                          // value dim (state columns)
-#ifndef BRAID_TILE_WAVES
-#define BRAID_TILE_WAVES 4
-#endif
-constexpr int kWaves = BRAID_TILE_WAVES;          // waves per tile (4 or 8)
-constexpr int kRowsPerWave = kSS / kWaves;        // 32
-constexpr int kChunks = kHD / 8;                  // 16 eight-column chunks per row
-constexpr int kRowGroups = 64 / kChunks;          // 4 row groups per wave
+constexpr int kSS = 128;                                 // key dim (state rows)
+constexpr int kHD = 128;                                 // value dim (state columns)
+constexpr int kWaves = 4;                                // row blocks per column group
+constexpr int kRowsPerWave = kSS / kWaves;               // 32
+constexpr int kRowGroups = 4;                            // row groups per wave (lane / 16)
+constexpr int kLanesPerRowGroup = 64 / kRowGroups;       // 16
 constexpr int kRowsPerLane = kRowsPerWave / kRowGroups;  // 8
-constexpr int kChunksPerWave = kChunks / kWaves;  // y chunks each wave stores
-constexpr int kTileThreads = 64 * kWaves;
 constexpr float kL2Eps = 1e-6f;
 // 128^-0.5 correctly rounded to fp32 (0x3DB504F3).
 constexpr float kYScale = 0.088388347648318440550f;
 
+// Threads of a tile's workgroup when each lane owns `cpl` columns.
+constexpr int tile_threads(int cpl) { return 64 * kWaves * (8 / cpl); }
+constexpr int kDecodeCols = 8;   // columns per lane, decode
+constexpr int kPrefillCols = 4;  // columns per lane, prefill
+
 // ---------------------------------------------------------------------------
-// Storage types. A Row8 is the eight consecutive elements of one state row a
-// lane owns, held in the pool's own encoding. load_nt / store_nt are the
+// Storage types. A Row<Tag, N> is the N consecutive elements of one state row
+// a lane owns, held in the pool's own encoding. load_nt / store_nt are the
 // streaming (nontemporal) accesses used for the state.
 
 struct F32 {};
 struct F16 {};
 struct BF16 {};
-
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // fp32 -> bf16 bits, round to nearest even; NaN -> 0x7FC0 (a quiet NaN).
 // Used for the activation-dtype round trip of the gates.
@@ -106,61 +110,55 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, bf16x2));
 }
 
-template <class Tag>
-struct Row8;
+template <class Tag, int N>
+struct Row;
 
-template <>
-struct Row8<F32> {
-  using elem = float;
-  f32x4 lo, hi;
+template <int N>
+struct Row<F32, N> {
+  typedef float vec __attribute__((ext_vector_type(N)));
+  vec d;
   __device__ __forceinline__ void load_nt(const float* p) {
-    lo = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
-    hi = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p + 4));
+    d = __builtin_nontemporal_load(reinterpret_cast<const vec*>(p));
   }
   __device__ __forceinline__ void store_nt(float* p) const {
-    __builtin_nontemporal_store(lo, reinterpret_cast<f32x4*>(p));
-    __builtin_nontemporal_store(hi, reinterpret_cast<f32x4*>(p + 4));
+    __builtin_nontemporal_store(d, reinterpret_cast<vec*>(p));
   }
-  __device__ __forceinline__ float get(int c) const { return c < 4 ? lo[c] : hi[c - 4]; }
+  __device__ __forceinline__ float get(int c) const { return d[c]; }
   // Columns c and c + 1 (c even).
   __device__ __forceinline__ void set2(int c, float x0, float x1) {
-    if (c < 4) {
-      lo[c] = x0;
-      lo[c + 1] = x1;
-    } else {
-      hi[c - 4] = x0;
-      hi[c - 3] = x1;
-    }
+    d[c] = x0;
+    d[c + 1] = x1;
   }
 };
 
-struct Row8Half {
-  using elem = uint16_t;
-  u32x4 raw;  // element c sits in bits 16*(c&1) of raw[c>>1]
+template <int N>
+struct RowHalf {
+  typedef uint32_t vec __attribute__((ext_vector_type(N / 2)));
+  vec raw;  // element c sits in bits 16*(c&1) of raw[c>>1]
   __device__ __forceinline__ void load_nt(const uint16_t* p) {
-    raw = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    raw = __builtin_nontemporal_load(reinterpret_cast<const vec*>(p));
   }
   __device__ __forceinline__ void store_nt(uint16_t* p) const {
-    __builtin_nontemporal_store(raw, reinterpret_cast<u32x4*>(p));
+    __builtin_nontemporal_store(raw, reinterpret_cast<vec*>(p));
   }
   __device__ __forceinline__ uint32_t bits(int c) const {
     return (raw[c >> 1] >> (16 * (c & 1))) & 0xffffu;
   }
 };
 
-template <>
-struct Row8<F16> : Row8Half {
-  __device__ __forceinline__ float get(int c) const { return f16_widen(bits(c)); }
+template <int N>
+struct Row<F16, N> : RowHalf<N> {
+  __device__ __forceinline__ float get(int c) const { return f16_widen(this->bits(c)); }
   __device__ __forceinline__ void set2(int c, float x0, float x1) {
-    raw[c >> 1] = pack_f16x2(x0, x1);
+    this->raw[c >> 1] = pack_f16x2(x0, x1);
   }
 };
 
-template <>
-struct Row8<BF16> : Row8Half {
-  __device__ __forceinline__ float get(int c) const { return bf16_widen(bits(c)); }
+template <int N>
+struct Row<BF16, N> : RowHalf<N> {
+  __device__ __forceinline__ float get(int c) const { return bf16_widen(this->bits(c)); }
   __device__ __forceinline__ void set2(int c, float x0, float x1) {
-    raw[c >> 1] = pack_bf16x2(x0, x1);
+    this->raw[c >> 1] = pack_bf16x2(x0, x1);
   }
 };
 
@@ -189,11 +187,11 @@ __device__ __forceinline__ float rowgroup_sum(float v) {
 
 // ---------------------------------------------------------------------------
 // Gate policies: where (alpha, beta) for (row b, head h, token t) come from.
-
+//
 // Each policy splits into load() — the global reads for (row b, head h,
-// token t) — and eval_alpha() / eval_beta() — the arithmetic — so a scan can issue the
-// next token's reads early, and so one wave can evaluate each gate for the
-// whole tile (publish_gates).
+// token t) — and eval_alpha() / eval_beta() — the arithmetic — so a scan can
+// issue the next token's reads early, and so one wave can evaluate each gate
+// for the whole tile (publish_gates).
 struct GateRaw {
   float x0, x1;  // policy-defined raw values
   bool pad;      // a pad column: alpha = 1, beta = 0
@@ -261,28 +259,35 @@ struct RawGates {
 };
 
 // ---------------------------------------------------------------------------
-// Lane geometry within a tile.
+// Lane geometry within a tile when each lane owns CPL columns (8 or 4).
+template <int CPL>
 struct LaneMap {
-  int wave;  // 0..kWaves-1: rows [kRowsPerWave wave, kRowsPerWave (wave + 1))
+  static constexpr int kGroupCols = kLanesPerRowGroup * CPL;  // columns per wave group
+  int wave;  // 0..(waves per tile - 1)
+  int w;     // row block 0..3: rows [32 w, 32 w + 32)
   int lane;  // 0..63
   int rg;    // row group 0..3
-  int c8;    // column chunk 0..15
-  int col0;  // first of this lane's eight columns
+  int cc;    // column chunk within the wave's column group, 0..15
+  int col0;  // first of this lane's CPL columns
   __device__ __forceinline__ LaneMap(int tid) {
     lane = tid & 63;
     wave = tid >> 6;
-    rg = lane / kChunks;
-    c8 = lane % kChunks;
-    col0 = c8 * 8;
+    w = wave % kWaves;
+    rg = lane / kLanesPerRowGroup;
+    cc = lane % kLanesPerRowGroup;
+    col0 = (wave / kWaves) * kGroupCols + cc * CPL;
   }
   __device__ __forceinline__ int row(int i) const {
-    return wave * kRowsPerWave + rg + kRowGroups * i;
+    return w * kRowsPerWave + rg + kRowGroups * i;
   }
+  // The lanes that write a column chunk's outputs: row group 0 of row block
+  // cc / 4 (the four row blocks share the stores).
+  __device__ __forceinline__ bool stores_y() const { return rg == 0 && cc / 4 == w; }
 };
 
-// Cross-wave exchange buffers for one tile: per-wave column partials of kv and
-// of y, kept apart so one token's y exchange never overwrites kv partials a
-// slower wave is still reading (and vice versa across tokens).
+// Cross-wave exchange buffers for one tile: per-row-block column partials of
+// kv and of y, kept apart so one token's y exchange never overwrites kv
+// partials a slower wave is still reading (and vice versa across tokens).
 struct TileLds {
   float kv[kWaves][kHD];
   float y[kWaves][kHD];
@@ -300,12 +305,13 @@ struct QK {
 };
 
 struct QKRaw {
-  float2 q2, k2;                   // elements 2 lane, 2 lane + 1 (for the norms)
-  float qr[kRowsPerLane];          // this lane's rows
+  float2 q2, k2;           // elements 2 lane, 2 lane + 1 (for the norms)
+  float qr[kRowsPerLane];  // this lane's rows
   float kr[kRowsPerLane];
 };
 
-__device__ __forceinline__ void load_qk(const LaneMap& L, const float* __restrict__ q,
+template <class LM>
+__device__ __forceinline__ void load_qk(const LM& L, const float* __restrict__ q,
                                         const float* __restrict__ k, QKRaw& r) {
   r.q2 = *reinterpret_cast<const float2*>(q + 2 * L.lane);
   r.k2 = *reinterpret_cast<const float2*>(k + 2 * L.lane);
@@ -328,94 +334,70 @@ __device__ __forceinline__ void normalize_qk(const QKRaw& r, QK& out) {
   }
 }
 
-__device__ __forceinline__ void normalize_qk(const LaneMap& L, const float* __restrict__ q,
+template <class LM>
+__device__ __forceinline__ void normalize_qk(const LM& L, const float* __restrict__ q,
                                              const float* __restrict__ k, QK& out) {
   QKRaw r;
   load_qk(L, q, k, r);
   normalize_qk(r, out);
 }
 
-// Completes a column sum: the lane's chain value `part` for columns
-// col0..col0+7 is reduced over the wave's row groups, exchanged through `buf`
-// and summed over the waves by a fixed pairwise tree. Every lane returns the
-// eight column totals of its chunk.
-__device__ __forceinline__ void tile_column_sums(const LaneMap& L, float (&part)[8],
+// Completes a column sum: the lane's chain values `part` for its CPL columns
+// are reduced over the wave's row groups, exchanged through `buf` and summed
+// over the four row blocks by the fixed pairwise tree (w0 + w1) + (w2 + w3).
+// Every lane returns the totals of its columns.
+template <int CPL>
+__device__ __forceinline__ void tile_column_sums(const LaneMap<CPL>& L, float (&part)[CPL],
                                                  float (*buf)[kHD]) {
+  typedef float vec __attribute__((ext_vector_type(CPL)));
 #pragma unroll
-  for (int c = 0; c < 8; ++c) part[c] = rowgroup_sum(part[c]);
+  for (int c = 0; c < CPL; ++c) part[c] = rowgroup_sum(part[c]);
   if (L.rg == 0) {
-    f32x4 lo, hi;
+    vec p;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      lo[c] = part[c];
-      hi[c] = part[c + 4];
-    }
-    *reinterpret_cast<f32x4*>(&buf[L.wave][L.col0]) = lo;
-    *reinterpret_cast<f32x4*>(&buf[L.wave][L.col0 + 4]) = hi;
+    for (int c = 0; c < CPL; ++c) p[c] = part[c];
+    *reinterpret_cast<vec*>(&buf[L.w][L.col0]) = p;
   }
   __syncthreads();
-  float w[kWaves][8];
+  vec wv[kWaves];
 #pragma unroll
-  for (int j = 0; j < kWaves; ++j) {
-    const f32x4 lo = *reinterpret_cast<const f32x4*>(&buf[j][L.col0]);
-    const f32x4 hi = *reinterpret_cast<const f32x4*>(&buf[j][L.col0 + 4]);
+  for (int j = 0; j < kWaves; ++j) wv[j] = *reinterpret_cast<const vec*>(&buf[j][L.col0]);
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      w[j][c] = lo[c];
-      w[j][c + 4] = hi[c];
-    }
-  }
-#pragma unroll
-  for (int c = 0; c < 8; ++c) {
-    float lvl[kWaves];
-#pragma unroll
-    for (int j = 0; j < kWaves; ++j) lvl[j] = w[j][c];
-#pragma unroll
-    for (int n = kWaves; n > 1; n >>= 1) {
-#pragma unroll
-      for (int j = 0; j < n / 2; ++j) lvl[j] = lvl[2 * j] + lvl[2 * j + 1];
-    }
-    part[c] = lvl[0];
-  }
+  for (int c = 0; c < CPL; ++c) part[c] = (wv[0][c] + wv[1][c]) + (wv[2][c] + wv[3][c]);
 }
 
-// True for the lanes that write a column chunk's outputs: row group 0 of the
-// wave assigned to that chunk (each wave stores kChunksPerWave chunks).
-__device__ __forceinline__ bool stores_y(const LaneMap& L) {
-  return L.rg == 0 && L.c8 / kChunksPerWave == L.wave;
-}
-
-// One token of the recurrence on this lane's 8 x 8 block. `v` holds the eight
+// One token of the recurrence on this lane's 8 x CPL block. `v` holds the
 // value entries of the lane's columns; `y` receives their outputs (identical
 // in every lane of a column chunk). alpha and beta are read from lds.gate
 // after the first barrier (publish_gates writes them before it). Contains two
 // workgroup barriers, so all waves of the tile must call it together.
-template <class Tag>
-__device__ __forceinline__ void gdn_token(const LaneMap& L, Row8<Tag> (&S)[kRowsPerLane],
-                                          const QK& qk, const float (&v)[8], TileLds& lds,
-                                          float (&y)[8]) {
-  float kv[8];
+template <class Tag, int CPL>
+__device__ __forceinline__ void gdn_token(const LaneMap<CPL>& L,
+                                          Row<Tag, CPL> (&S)[kRowsPerLane], const QK& qk,
+                                          const float (&v)[CPL], TileLds& lds,
+                                          float (&y)[CPL]) {
+  float kv[CPL];
 #pragma unroll
-  for (int c = 0; c < 8; ++c) kv[c] = S[0].get(c) * qk.kh[0];
+  for (int c = 0; c < CPL; ++c) kv[c] = S[0].get(c) * qk.kh[0];
 #pragma unroll
   for (int i = 1; i < kRowsPerLane; ++i) {
 #pragma unroll
-    for (int c = 0; c < 8; ++c) kv[c] = fmaf(S[i].get(c), qk.kh[i], kv[c]);
+    for (int c = 0; c < CPL; ++c) kv[c] = fmaf(S[i].get(c), qk.kh[i], kv[c]);
   }
-  tile_column_sums(L, kv, lds.kv);
+  tile_column_sums<CPL>(L, kv, lds.kv);
   const float alpha = lds.gate[0];
   const float beta = lds.gate[1];
-  float delta[8];
+  float delta[CPL];
 #pragma unroll
-  for (int c = 0; c < 8; ++c) delta[c] = (v[c] - alpha * kv[c]) * beta;
+  for (int c = 0; c < CPL; ++c) delta[c] = (v[c] - alpha * kv[c]) * beta;
 
-  float acc[8];
+  float acc[CPL];
 #pragma unroll
-  for (int c = 0; c < 8; ++c) acc[c] = 0.f;
+  for (int c = 0; c < CPL; ++c) acc[c] = 0.f;
 #pragma unroll
   for (int i = 0; i < kRowsPerLane; ++i) {
 #pragma unroll
-    for (int c = 0; c < 8; c += 2) {
+    for (int c = 0; c < CPL; c += 2) {
       // S' = alpha * S + k_hat * delta, contracted as fma(alpha, S, k_hat * delta):
       // the 16-bit S feeds the fma directly (v_fma_mix, exact widening), one
       // instruction fewer per element than widening, scaling, then fusing.
@@ -426,19 +408,19 @@ __device__ __forceinline__ void gdn_token(const LaneMap& L, Row8<Tag> (&S)[kRows
       acc[c + 1] = fmaf(n1, qk.qh[i], acc[c + 1]);
     }
   }
-  tile_column_sums(L, acc, lds.y);
+  tile_column_sums<CPL>(L, acc, lds.y);
 #pragma unroll
-  for (int c = 0; c < 8; ++c) y[c] = acc[c] * kYScale;
+  for (int c = 0; c < CPL; ++c) y[c] = acc[c] * kYScale;
 }
 
 // Computes one token's gates ONCE per tile and leaves them in lds.gate for
 // gdn_token: wave 0 evaluates alpha (exp, log1p, exp), wave 1 beta (exp and a
 // divide), each from the raw values all waves loaded. The next workgroup
-// barrier publishes them. The arithmetic is the policy's own (Gates::eval_alpha /
-// Gates::eval_beta), so which wave runs it does not change a bit.
-template <class Gates>
-__device__ __forceinline__ void publish_gates(const LaneMap& L, const Gates& gates,
-                                              const GateRaw& r, int h, TileLds& lds) {
+// barrier publishes them. The arithmetic is the policy's own (eval_alpha /
+// eval_beta), so which wave runs it does not change a bit.
+template <class Gates, class LM>
+__device__ __forceinline__ void publish_gates(const LM& L, const Gates& gates, const GateRaw& r,
+                                              int h, TileLds& lds) {
   if (L.wave == 0) {
     const float a = gates.eval_alpha(r, h);
     if (L.lane == 0) lds.gate[0] = a;
@@ -448,25 +430,21 @@ __device__ __forceinline__ void publish_gates(const LaneMap& L, const Gates& gat
   }
 }
 
-__device__ __forceinline__ void load8(const float* __restrict__ p, float (&out)[8]) {
-  const f32x4 a = *reinterpret_cast<const f32x4*>(p);
-  const f32x4 b = *reinterpret_cast<const f32x4*>(p + 4);
+template <int N>
+__device__ __forceinline__ void loadN(const float* __restrict__ p, float (&out)[N]) {
+  typedef float vec __attribute__((ext_vector_type(N)));
+  const vec a = *reinterpret_cast<const vec*>(p);
 #pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    out[c] = a[c];
-    out[c + 4] = b[c];
-  }
+  for (int c = 0; c < N; ++c) out[c] = a[c];
 }
 
-__device__ __forceinline__ void store8(float* __restrict__ p, const float (&in)[8]) {
-  f32x4 a, b;
+template <int N>
+__device__ __forceinline__ void storeN(float* __restrict__ p, const float (&in)[N]) {
+  typedef float vec __attribute__((ext_vector_type(N)));
+  vec a;
 #pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    a[c] = in[c];
-    b[c] = in[c + 4];
-  }
-  *reinterpret_cast<f32x4*>(p) = a;
-  *reinterpret_cast<f32x4*>(p + 4) = b;
+  for (int c = 0; c < N; ++c) a[c] = in[c];
+  *reinterpret_cast<vec*>(p) = a;
 }
 
 }  // namespace braid

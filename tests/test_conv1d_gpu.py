@@ -213,3 +213,20 @@ def test_prefill_rejects_duplicate_slots_and_handles_no_seq_lens(kern):
     kern.conv1d_prefill(p2, slots, x, w, bias, o2,
                         torch.full((B,), T, dtype=torch.int32, device=DEV))
     assert torch.equal(o1, o2) and torch.equal(p1, p2)
+
+
+def test_prefill_scalar_channel_path_equals_decode(kern):
+    """C not a multiple of 4 takes the one-channel-per-thread path."""
+    B, T, C, K = 2, 19, 258, 4
+    pool0, x, w, bias = _prefill_inputs(B, T, C, K, torch.bfloat16, seed=21)
+    slots = torch.tensor([3, 1], dtype=torch.int32, device=DEV)
+    lens = torch.tensor([19, 7], dtype=torch.int32, device=DEV)
+    pp, pd = pool0.clone(), pool0.clone()
+    out = torch.empty(B, T, C, device=DEV)
+    kern.conv1d_prefill(pp, slots, x, w, bias, out, lens)
+    for t in range(T):
+        live = [b for b in range(B) if t < int(lens[b])]
+        o = torch.empty(len(live), C, device=DEV)
+        kern.conv1d_decode(pd, slots[live].contiguous(), x[live, t].contiguous(), w, bias, o)
+        assert torch.equal(o, out[live, t])
+    assert torch.equal(pp, pd)
