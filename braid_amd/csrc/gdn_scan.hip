@@ -56,7 +56,7 @@ gdn_decode_kernel(typename Storage<Tag>::T* __restrict__ pool, const int* __rest
   publish_gates(L, gates, gates.load(b, h, 0, H, 1), h, lds);
 
   float yy[CPL];
-  gdn_token<Tag, CPL>(L, S, qk, vv, lds, yy);
+  gdn_token<Tag, CPL>(L, S, qk, vv, lds, lds.gate, yy);
 
 #pragma unroll
   for (int i = 0; i < kRowsPerLane; ++i) S[i].store_nt(tile + (size_t)L.row(i) * kHD);
@@ -64,9 +64,60 @@ gdn_decode_kernel(typename Storage<Tag>::T* __restrict__ pool, const int* __rest
   if (L.stores_y()) storeN<CPL>(y + ((size_t)b * H + h) * kHD + L.col0, yy);
 }
 
+// Per-token values of a prefill chunk that do not depend on the state.
+constexpr int kScanChunk = 256;
+struct ChunkLds {
+  float gate[kScanChunk][2];  // alpha, beta
+  float inv[kScanChunk][2];   // 1/|q|, 1/|k| (with the 1e-6 epsilon)
+};
+
+// Fills `cl` for tokens [t0, t0 + n) of row b, head h: every thread evaluates
+// one token's gates (the policy's own arithmetic, as publish_gates runs it),
+// and each wave computes the q/k norm factors of every (waves)-th token with
+// the same 64-lane butterfly as the decode kernel's normalize_qk, two tokens at
+// a time so the two shuffle chains overlap. Same values, same bits.
+template <class Gates, int CPL>
+__device__ __forceinline__ void scan_chunk_prologue(const LaneMap<CPL>& L, const Gates& gates,
+                                                    const float* __restrict__ q,
+                                                    const float* __restrict__ k, int b, int h,
+                                                    int g, int H, int G, int T, int t0, int n,
+                                                    ChunkLds& cl) {
+  constexpr int kThreads = tile_threads(CPL);
+  constexpr int kTileWaves = kThreads / 64;
+  for (int j = threadIdx.x; j < n; j += kThreads) {
+    const GateRaw r = gates.load(b, h, t0 + j, H, T);
+    cl.gate[j][0] = gates.eval_alpha(r, h);
+    cl.gate[j][1] = gates.eval_beta(r);
+  }
+  for (int j = L.wave; j < n; j += 2 * kTileWaves) {
+    const int j2 = j + kTileWaves;
+    const size_t o1 = (((size_t)b * T + t0 + j) * G + g) * kSS + 2 * L.lane;
+    const float2 q1 = *reinterpret_cast<const float2*>(q + o1);
+    const float2 k1 = *reinterpret_cast<const float2*>(k + o1);
+    float2 q2 = make_float2(0.f, 0.f), k2 = make_float2(0.f, 0.f);
+    if (j2 < n) {
+      const size_t o2 = (((size_t)b * T + t0 + j2) * G + g) * kSS + 2 * L.lane;
+      q2 = *reinterpret_cast<const float2*>(q + o2);
+      k2 = *reinterpret_cast<const float2*>(k + o2);
+    }
+    const float qi1 = inv_norm(q1), ki1 = inv_norm(k1);
+    const float qi2 = inv_norm(q2), ki2 = inv_norm(k2);
+    if (L.lane == 0) {
+      cl.inv[j][0] = qi1;
+      cl.inv[j][1] = ki1;
+      if (j2 < n) {
+        cl.inv[j2][0] = qi2;
+        cl.inv[j2][1] = ki2;
+      }
+    }
+  }
+}
+
 // T tokens for the tile with the state resident in registers, in the column-
 // split layout (4 columns per lane, eight waves): the same per-column
-// arithmetic as the decode kernel, token by token.
+// arithmetic as the decode kernel, token by token. Tokens are processed in
+// chunks of kScanChunk: a parallel prologue computes the chunk's gates and q/k
+// norm factors into LDS, so the serial loop carries only the recurrence.
 template <class Tag, class Gates>
 __global__ void __launch_bounds__(tile_threads(kPrefillCols))
 gdn_prefill_kernel(typename Storage<Tag>::T* __restrict__ pool,
@@ -82,6 +133,7 @@ gdn_prefill_kernel(typename Storage<Tag>::T* __restrict__ pool,
   const LaneMap<CPL> L(threadIdx.x);
 
   __shared__ TileLds lds;
+  __shared__ ChunkLds cl;
   const int slot = slot_idx[b];
   ST* tile = pool + ((size_t)slot * H + h) * (kSS * kHD) + L.col0;
 
@@ -89,41 +141,38 @@ gdn_prefill_kernel(typename Storage<Tag>::T* __restrict__ pool,
 #pragma unroll
   for (int i = 0; i < kRowsPerLane; ++i) S[i].load_nt(tile + (size_t)L.row(i) * kHD);
 
-  // Software pipeline: token t + 1's inputs are loaded while token t's
-  // recurrence runs, and its q/k norms and gates are evaluated right after;
-  // none of them depends on the state. (Evaluating them between token t's two
-  // barriers instead measured slower: wave 0's gate math then stalls the
-  // other waves at the second barrier.)
-  QK qk;
-  float vv[CPL];
-  if (T > 0) {
+  for (int t0 = 0; t0 < T; t0 += kScanChunk) {
+    const int n = min(kScanChunk, T - t0);
+    // The previous chunk's last token ended with a barrier after its last LDS
+    // reads, so the prologue may overwrite `cl`; this barrier publishes it.
+    scan_chunk_prologue(L, gates, q, k, b, h, g, H, G, T, t0, n, cl);
+    __syncthreads();
+
+    // Inputs of token t + 1 are loaded while token t runs.
     QKRaw raw;
-    load_qk(L, q + ((size_t)b * T * G + g) * kSS, k + ((size_t)b * T * G + g) * kSS, raw);
-    loadN<CPL>(v + ((size_t)b * T * H + h) * kHD + L.col0, vv);
-    publish_gates(L, gates, gates.load(b, h, 0, H, T), h, lds);
-    normalize_qk(raw, qk);
-  }
-  for (int t = 0; t < T; ++t) {
-    const size_t bt_idx = (size_t)b * T + t;
-    const bool more = t + 1 < T;
-    QKRaw raw_n;
-    GateRaw gate_n{};
-    float vv_n[CPL];
-    if (more) {
-      load_qk(L, q + ((bt_idx + 1) * G + g) * kSS, k + ((bt_idx + 1) * G + g) * kSS, raw_n);
-      loadN<CPL>(v + ((bt_idx + 1) * H + h) * kHD + L.col0, vv_n);
-      gate_n = gates.load(b, h, t + 1, H, T);
-    }
-    float yy[CPL];
-    gdn_token<Tag, CPL>(L, S, qk, vv, lds, yy);
-    if (L.stores_y()) storeN<CPL>(y + (bt_idx * H + h) * kHD + L.col0, yy);
-    if (more) {
-      // lds.gate was last read before this token's second barrier: safe to
-      // overwrite; the next token's first barrier publishes the new values.
-      publish_gates(L, gates, gate_n, h, lds);
-      normalize_qk(raw_n, qk);
+    float vv[CPL];
+    load_qk(L, q + (((size_t)b * T + t0) * G + g) * kSS, k + (((size_t)b * T + t0) * G + g) * kSS,
+            raw);
+    loadN<CPL>(v + (((size_t)b * T + t0) * H + h) * kHD + L.col0, vv);
+    for (int j = 0; j < n; ++j) {
+      const size_t bt_idx = (size_t)b * T + t0 + j;
+      const bool more = j + 1 < n;
+      QKRaw raw_n;
+      float vv_n[CPL];
+      if (more) {
+        load_qk(L, q + ((bt_idx + 1) * G + g) * kSS, k + ((bt_idx + 1) * G + g) * kSS, raw_n);
+        loadN<CPL>(v + ((bt_idx + 1) * H + h) * kHD + L.col0, vv_n);
+      }
+      QK qk;
+      scale_qk(raw, cl.inv[j][0], cl.inv[j][1], qk);
+      float yy[CPL];
+      gdn_token<Tag, CPL>(L, S, qk, vv, lds, cl.gate[j], yy);
+      if (L.stores_y()) storeN<CPL>(y + (bt_idx * H + h) * kHD + L.col0, yy);
+      if (more) {
+        raw = raw_n;
 #pragma unroll
-      for (int c = 0; c < CPL; ++c) vv[c] = vv_n[c];
+        for (int c = 0; c < CPL; ++c) vv[c] = vv_n[c];
+      }
     }
   }
 

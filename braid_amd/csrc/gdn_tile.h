@@ -322,16 +322,22 @@ __device__ __forceinline__ void load_qk(const LM& L, const float* __restrict__ q
   }
 }
 
-__device__ __forceinline__ void normalize_qk(const QKRaw& r, QK& out) {
-  const float qs = wave_sum(r.q2.x * r.q2.x + r.q2.y * r.q2.y);
-  const float ks = wave_sum(r.k2.x * r.k2.x + r.k2.y * r.k2.y);
-  const float q_inv = rsqrtf(qs + kL2Eps);
-  const float k_inv = rsqrtf(ks + kL2Eps);
+// 1 / sqrt(sum x^2 + 1e-6) of a [128] vector held as x[2 lane], x[2 lane + 1]
+// by the 64 lanes of a wave; every lane returns the same bits.
+__device__ __forceinline__ float inv_norm(float2 x2) {
+  return rsqrtf(wave_sum(x2.x * x2.x + x2.y * x2.y) + kL2Eps);
+}
+
+__device__ __forceinline__ void scale_qk(const QKRaw& r, float q_inv, float k_inv, QK& out) {
 #pragma unroll
   for (int i = 0; i < kRowsPerLane; ++i) {
     out.qh[i] = r.qr[i] * q_inv;
     out.kh[i] = r.kr[i] * k_inv;
   }
+}
+
+__device__ __forceinline__ void normalize_qk(const QKRaw& r, QK& out) {
+  scale_qk(r, inv_norm(r.q2), inv_norm(r.k2), out);
 }
 
 template <class LM>
@@ -368,14 +374,15 @@ __device__ __forceinline__ void tile_column_sums(const LaneMap<CPL>& L, float (&
 
 // One token of the recurrence on this lane's 8 x CPL block. `v` holds the
 // value entries of the lane's columns; `y` receives their outputs (identical
-// in every lane of a column chunk). alpha and beta are read from lds.gate
-// after the first barrier (publish_gates writes them before it). Contains two
+// in every lane of a column chunk). alpha and beta are read from LDS at
+// `gate` ([alpha, beta]) after the first barrier, so whoever writes them must
+// do so before it (publish_gates, or a scan's per-chunk prologue). Contains two
 // workgroup barriers, so all waves of the tile must call it together.
 template <class Tag, int CPL>
 __device__ __forceinline__ void gdn_token(const LaneMap<CPL>& L,
                                           Row<Tag, CPL> (&S)[kRowsPerLane], const QK& qk,
                                           const float (&v)[CPL], TileLds& lds,
-                                          float (&y)[CPL]) {
+                                          const float* gate, float (&y)[CPL]) {
   float kv[CPL];
 #pragma unroll
   for (int c = 0; c < CPL; ++c) kv[c] = S[0].get(c) * qk.kh[0];
@@ -385,8 +392,8 @@ __device__ __forceinline__ void gdn_token(const LaneMap<CPL>& L,
     for (int c = 0; c < CPL; ++c) kv[c] = fmaf(S[i].get(c), qk.kh[i], kv[c]);
   }
   tile_column_sums<CPL>(L, kv, lds.kv);
-  const float alpha = lds.gate[0];
-  const float beta = lds.gate[1];
+  const float alpha = gate[0];
+  const float beta = gate[1];
   float delta[CPL];
 #pragma unroll
   for (int c = 0; c < CPL; ++c) delta[c] = (v[c] - alpha * kv[c]) * beta;
