@@ -348,12 +348,15 @@ __device__ __forceinline__ void normalize_qk(const LM& L, const float* __restric
   normalize_qk(r, out);
 }
 
-// Completes a column sum: the lane's chain values `part` for its CPL columns
-// are reduced over the wave's row groups, exchanged through `buf` and summed
-// over the four row blocks by the fixed pairwise tree (w0 + w1) + (w2 + w3).
-// Every lane returns the totals of its columns.
+// Column sums of the tile are completed in two halves around a workgroup
+// barrier, so a scan can put two sums behind ONE barrier:
+//   column_sums_post:  reduce the lane's chain values over the wave's row
+//                      groups and (row group 0) write them to buf[row block];
+//   column_sums_take:  after the barrier, read the four row blocks' partials
+//                      and add them by the fixed tree (w0 + w1) + (w2 + w3).
+// Every lane ends with the totals of its columns.
 template <int CPL>
-__device__ __forceinline__ void tile_column_sums(const LaneMap<CPL>& L, float (&part)[CPL],
+__device__ __forceinline__ void column_sums_post(const LaneMap<CPL>& L, float (&part)[CPL],
                                                  float (*buf)[kHD]) {
   typedef float vec __attribute__((ext_vector_type(CPL)));
 #pragma unroll
@@ -364,7 +367,12 @@ __device__ __forceinline__ void tile_column_sums(const LaneMap<CPL>& L, float (&
     for (int c = 0; c < CPL; ++c) p[c] = part[c];
     *reinterpret_cast<vec*>(&buf[L.w][L.col0]) = p;
   }
-  __syncthreads();
+}
+
+template <int CPL>
+__device__ __forceinline__ void column_sums_take(const LaneMap<CPL>& L, float (&part)[CPL],
+                                                 float (*buf)[kHD]) {
+  typedef float vec __attribute__((ext_vector_type(CPL)));
   vec wv[kWaves];
 #pragma unroll
   for (int j = 0; j < kWaves; ++j) wv[j] = *reinterpret_cast<const vec*>(&buf[j][L.col0]);
@@ -372,18 +380,11 @@ __device__ __forceinline__ void tile_column_sums(const LaneMap<CPL>& L, float (&
   for (int c = 0; c < CPL; ++c) part[c] = (wv[0][c] + wv[1][c]) + (wv[2][c] + wv[3][c]);
 }
 
-// One token of the recurrence on this lane's 8 x CPL block. `v` holds the
-// value entries of the lane's columns; `y` receives their outputs (identical
-// in every lane of a column chunk). alpha and beta are read from LDS at
-// `gate` ([alpha, beta]) after the first barrier, so whoever writes them must
-// do so before it (publish_gates, or a scan's per-chunk prologue). Contains two
-// workgroup barriers, so all waves of the tile must call it together.
+// kv chain of one token: kv[c] = sum over the lane's eight rows of
+// S[i][c] * k_hat[i], in row order.
 template <class Tag, int CPL>
-__device__ __forceinline__ void gdn_token(const LaneMap<CPL>& L,
-                                          Row<Tag, CPL> (&S)[kRowsPerLane], const QK& qk,
-                                          const float (&v)[CPL], TileLds& lds,
-                                          const float* gate, float (&y)[CPL]) {
-  float kv[CPL];
+__device__ __forceinline__ void kv_partials(const Row<Tag, CPL> (&S)[kRowsPerLane], const QK& qk,
+                                            float (&kv)[CPL]) {
 #pragma unroll
   for (int c = 0; c < CPL; ++c) kv[c] = S[0].get(c) * qk.kh[0];
 #pragma unroll
@@ -391,14 +392,17 @@ __device__ __forceinline__ void gdn_token(const LaneMap<CPL>& L,
 #pragma unroll
     for (int c = 0; c < CPL; ++c) kv[c] = fmaf(S[i].get(c), qk.kh[i], kv[c]);
   }
-  tile_column_sums<CPL>(L, kv, lds.kv);
-  const float alpha = gate[0];
-  const float beta = gate[1];
+}
+
+// The update phase of one token, given the column totals kv: delta, the state
+// update narrowed to the storage type, and the readout's chain values.
+template <class Tag, int CPL>
+__device__ __forceinline__ void update_state(Row<Tag, CPL> (&S)[kRowsPerLane], const QK& qk,
+                                             const float (&v)[CPL], const float (&kv)[CPL],
+                                             float alpha, float beta, float (&acc)[CPL]) {
   float delta[CPL];
 #pragma unroll
   for (int c = 0; c < CPL; ++c) delta[c] = (v[c] - alpha * kv[c]) * beta;
-
-  float acc[CPL];
 #pragma unroll
   for (int c = 0; c < CPL; ++c) acc[c] = 0.f;
 #pragma unroll
@@ -415,7 +419,29 @@ __device__ __forceinline__ void gdn_token(const LaneMap<CPL>& L,
       acc[c + 1] = fmaf(n1, qk.qh[i], acc[c + 1]);
     }
   }
-  tile_column_sums<CPL>(L, acc, lds.y);
+}
+
+// One token of the recurrence on this lane's 8 x CPL block. `v` holds the
+// value entries of the lane's columns; `y` receives their outputs (identical
+// in every lane of a column chunk). alpha and beta are read from LDS at
+// `gate` ([alpha, beta]) after the first barrier, so whoever writes them must
+// do so before it (publish_gates). Contains two workgroup barriers, so all
+// waves of the tile must call it together.
+template <class Tag, int CPL>
+__device__ __forceinline__ void gdn_token(const LaneMap<CPL>& L,
+                                          Row<Tag, CPL> (&S)[kRowsPerLane], const QK& qk,
+                                          const float (&v)[CPL], TileLds& lds,
+                                          const float* gate, float (&y)[CPL]) {
+  float kv[CPL];
+  kv_partials<Tag, CPL>(S, qk, kv);
+  column_sums_post<CPL>(L, kv, lds.kv);
+  __syncthreads();
+  column_sums_take<CPL>(L, kv, lds.kv);
+  float acc[CPL];
+  update_state<Tag, CPL>(S, qk, v, kv, gate[0], gate[1], acc);
+  column_sums_post<CPL>(L, acc, lds.y);
+  __syncthreads();
+  column_sums_take<CPL>(L, acc, lds.y);
 #pragma unroll
   for (int c = 0; c < CPL; ++c) y[c] = acc[c] * kYScale;
 }
