@@ -30,8 +30,11 @@ BASELINE shapes, each captured in a hipGraph and timed with events:
                     (bytes: bf16 x in, fp32 out over the padded [8, T, 8192])
   conv1d_decode     B=64, C=8192, K=4, bf16 in (HBM bytes per the layout)
   quantize_act      [64, 4096] bf16 (both launches)
-  mixer_step        config 3: 24 GDN layers of quant -> conv -> gated decode at
-                    B=64, one fp16 pool and conv pool per layer
+  readout_quant_*   gated RMSNorm readout + out_proj input FP8 quant (both
+                    launches), 64 decode tokens and config 2's 4073 tokens
+  mixer_step        config 3: 24 GDN layers of quant -> conv -> gated decode ->
+                    readout + quant at B=64, one fp16 pool and conv pool per
+                    layer
   mixed_tick        config 4: 4 x 256-token prefill + 96 decode rows on one
                     192-slot fp16 pool; eager and graph-replayed per bucket
 
@@ -184,6 +187,9 @@ CONV_BYTES_B64 = (64 * 8192 * 3 * 4 + 64 * 8192 * 4 * 4 + 64 * 8192 * 2 + 64 * 8
                   + 8192 * 4 * 4 + 8192 * 4)
 QUANT_BYTES_64x4096 = 64 * 4096 * 2 + 64 * 4096 + 4
 ROW_BYTES = 2 * H * D * D * 2 + (2 * G * D + 2 * H * D) * 4 + H * 2 * 2 + 4
+# readout per element: y fp32 + z bf16 read, core bf16 written and read back
+# by the quantize pass, fp8 code written
+READOUT_BYTES_PER_ELEM = 4 + 2 + 2 + 2 + 1
 
 
 def graph_time(torch, fn, reps=5, inner=1, before_replay=None):
@@ -284,6 +290,20 @@ def measure_paths(torch, kern):
     out["quantize_act"] = {"shape": "64x4096 bf16", "us": round(t * 1e6, 2),
                            "gbs": round(QUANT_BYTES_64x4096 / t / 1e9, 1)}
 
+    # gated RMSNorm readout + out_proj input quant: decode (64 tokens) and
+    # config 2's prefill (4073 tokens); y fp32, z/core bf16, q fp8
+    gamma = 1.0 + 0.3 * torch.randn(D, generator=g, device=dev)
+    for label, ntok in (("readout_quant_b64", 64), ("readout_quant_prefill", sum(lens))):
+        ry = torch.randn(ntok, H, D, generator=g, device=dev)
+        rz = torch.randn(ntok, H * D, generator=g, device=dev).to(torch.bfloat16)
+        t = graph_time(torch, lambda: kern.gated_rmsnorm(ry, rz, gamma, 1e-6), reps=5,
+                       inner=20 if ntok == 64 else 1)
+        rbytes = ntok * H * D * READOUT_BYTES_PER_ELEM
+        out[label] = {"tokens": ntok, "us": round(t * 1e6, 2),
+                      "gbs": round(rbytes / t / 1e9, 1),
+                      "hbm_frac": round(rbytes / t / 1e9 / HBM_PEAK_GBS, 4)}
+        del ry, rz
+
     # config 3: 24-layer mixer decode step at B=64
     L, Bm, S = 24, 64, 72
     layers = []
@@ -297,7 +317,8 @@ def measure_paths(torch, kern):
             xin=torch.randn(Bm, C, generator=g, device=dev).to(torch.bfloat16),
             a=torch.randn(Bm, H, generator=g, device=dev).to(torch.bfloat16),
             b=torch.randn(Bm, H, generator=g, device=dev).to(torch.bfloat16),
-            cout=torch.empty(Bm, C, device=dev), y=torch.empty(Bm, H, D, device=dev)))
+            cout=torch.empty(Bm, C, device=dev), y=torch.empty(Bm, H, D, device=dev),
+            z=torch.randn(Bm, H * D, generator=g, device=dev).to(torch.bfloat16)))
 
     def mixer_step():
         for ly in layers:
@@ -307,9 +328,11 @@ def measure_paths(torch, kern):
             kern.gdn_decode_raw(ly["pool"], slots64, q.unflatten(-1, (G, D)),
                                 k.unflatten(-1, (G, D)), v.unflatten(-1, (H, D)), ly["a"],
                                 ly["b"], A, dtb, ly["y"])
+            kern.gated_rmsnorm(ly["y"], ly["z"], gamma, 1e-6)
 
     t = graph_time(torch, mixer_step, reps=5)
-    step_bytes = L * (QUANT_BYTES_64x4096 + CONV_BYTES_B64 + Bm * ROW_BYTES)
+    step_bytes = L * (QUANT_BYTES_64x4096 + CONV_BYTES_B64 + Bm * ROW_BYTES
+                      + Bm * H * D * READOUT_BYTES_PER_ELEM)
     out["mixer_step"] = {"layers": L, "batch": Bm, "us": round(t * 1e6, 1),
                          "gbs": round(step_bytes / t / 1e9, 1),
                          "hbm_frac": round(step_bytes / t / 1e9 / HBM_PEAK_GBS, 4),

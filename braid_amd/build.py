@@ -29,7 +29,8 @@ ROOT = PKG.parent
 LIB = PKG / "libbraid_gdn.so"
 OBJ_DIR = PKG / "_build"
 
-SOURCES = ["capi_common.cpp", "gdn_scan.hip", "conv1d_decode.hip", "quant_act.hip"]
+SOURCES = ["capi_common.cpp", "gdn_scan.hip", "conv1d_decode.hip", "quant_act.hip",
+           "gated_norm.hip"]
 
 ARCH = os.environ.get("BRAID_OFFLOAD_ARCH", "gfx950")
 

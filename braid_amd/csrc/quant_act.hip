@@ -21,158 +21,12 @@
 // redundant re-reduction — and converts its share. 128-bit loads throughout:
 // eight bf16/fp16 elements (or two vectors of four fp32) per thread-iteration,
 // eight fp8 codes per 64-bit store.
-#include "capi_common.h"
+#include "quant_common.h"
 
 namespace braid {
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kVec = 8;
-constexpr int kMaxBlocks = 1024;
-constexpr float kFp8Max = 448.0f;
-constexpr float kInvFp8Max = 1.0f / 448.0f;  // fl32(1/448), as torch's scalar division rounds it
-constexpr float kEps = 1e-12f;
-
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-
-struct XF32 { using T = float; };
-struct XF16 { using T = uint16_t; };
-struct XBF16 { using T = uint16_t; };
-
-__device__ __forceinline__ float widen(XF32, float v) { return v; }
-__device__ __forceinline__ float widen(XF16, uint16_t v) {
-  return (float)__builtin_bit_cast(_Float16, v);
-}
-__device__ __forceinline__ float widen(XBF16, uint16_t v) {
-  return __uint_as_float((uint32_t)v << 16);
-}
-
-// Loads eight consecutive elements starting at x[i] (16-byte aligned).
-__device__ __forceinline__ void load_vec(XF32, const float* x, long i, float (&o)[kVec]) {
-  const f32x4 a = *reinterpret_cast<const f32x4*>(x + i);
-  const f32x4 b = *reinterpret_cast<const f32x4*>(x + i + 4);
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    o[j] = a[j];
-    o[j + 4] = b[j];
-  }
-}
-template <class Tag>
-__device__ __forceinline__ void load_vec(Tag tag, const uint16_t* x, long i, float (&o)[kVec]) {
-  const u32x4 r = *reinterpret_cast<const u32x4*>(x + i);
-#pragma unroll
-  for (int j = 0; j < kVec; ++j)
-    o[j] = widen(tag, (uint16_t)((r[j >> 1] >> (16 * (j & 1))) & 0xffffu));
-}
-
-// NaN-propagating max: once m is NaN it stays NaN.
-__device__ __forceinline__ float nan_max(float m, float v) { return (v != v || v > m) ? v : m; }
-
-__device__ __forceinline__ float block_nan_max(float m) {
-  __shared__ float waves[kThreads / 64];
-#pragma unroll
-  for (int s = 1; s < 64; s <<= 1) m = nan_max(m, __shfl_xor(m, s, 64));
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  if (lane == 0) waves[wave] = m;
-  __syncthreads();
-  float r = waves[0];
-#pragma unroll
-  for (int w = 1; w < kThreads / 64; ++w) r = nan_max(r, waves[w]);
-  return r;
-}
-
-// fp32 -> e4m3fn code, round to nearest even.
-//   |f| >= 480 or NaN       -> 0x7f (NaN)
-//   2^-6 <= |f| < 480       -> round the fp32 mantissa to 3 bits (RNE), rebias
-//                              the exponent from 127 to 7; a mantissa carry
-//                              rolls into the exponent, and (464, 480) lands on
-//                              0x7f exactly as the RNE rule puts it past 448
-//   |f| < 2^-6              -> subnormal: the code is |f| / 2^-9 rounded to an
-//                              integer (RNE), 0..8 (8 is the smallest normal)
-__device__ __forceinline__ uint32_t e4m3fn_code(float f) {
-  const uint32_t u = __float_as_uint(f);
-  const uint32_t sign = (u >> 24) & 0x80u;
-  const uint32_t a = u & 0x7fffffffu;
-  uint32_t code;
-  if (a >= 0x43f00000u) {            // 480.0f, and every Inf/NaN pattern above it
-    code = 0x7fu;
-  } else if (a < 0x3c800000u) {      // 2^-6
-    code = (uint32_t)rintf(__uint_as_float(a) * 512.0f);
-  } else {
-    const uint32_t r = a + 0x7ffffu + ((a >> 20) & 1u);
-    code = (r >> 20) - ((127u - 7u) << 3);
-  }
-  return code | sign;
-}
-
-__device__ __forceinline__ float quant_value(float x, float sc) {
-  float v = x / sc;
-  v = (v < -kFp8Max) ? -kFp8Max : ((v > kFp8Max) ? kFp8Max : v);
-  return v;
-}
-
-template <class Tag>
-__global__ void __launch_bounds__(kThreads)
-amax_partial(const typename Tag::T* __restrict__ x, float* __restrict__ partial, long n,
-             int vec) {
-  const long tid = (long)blockIdx.x * kThreads + threadIdx.x;
-  const long stride = (long)gridDim.x * kThreads;
-  float m = 0.f;
-  long tail = 0;
-  if (vec) {
-    const long nv = n / kVec;
-    for (long j = tid; j < nv; j += stride) {
-      float o[kVec];
-      load_vec(Tag{}, x, j * kVec, o);
-#pragma unroll
-      for (int e = 0; e < kVec; ++e) m = nan_max(m, fabsf(o[e]));
-    }
-    tail = nv * kVec;
-  }
-  for (long i = tail + tid; i < n; i += stride) m = nan_max(m, fabsf(widen(Tag{}, x[i])));
-  m = block_nan_max(m);
-  if (threadIdx.x == 0) partial[blockIdx.x] = m;
-}
-
-template <class Tag>
-__global__ void __launch_bounds__(kThreads)
-quantize(const typename Tag::T* __restrict__ x, const float* __restrict__ partial, int nparts,
-         float* __restrict__ scale, uint8_t* __restrict__ q, long n, int vec) {
-  float m = 0.f;
-  for (int i = threadIdx.x; i < nparts; i += kThreads) m = nan_max(m, partial[i]);
-  m = block_nan_max(m);
-  const float raw = m * kInvFp8Max;
-  const float sc = (raw < kEps) ? kEps : raw;
-  if (blockIdx.x == 0 && threadIdx.x == 0) scale[0] = sc;
-
-  const long tid = (long)blockIdx.x * kThreads + threadIdx.x;
-  const long stride = (long)gridDim.x * kThreads;
-  long tail = 0;
-  if (vec) {
-    const long nv = n / kVec;
-    for (long j = tid; j < nv; j += stride) {
-      float o[kVec];
-      load_vec(Tag{}, x, j * kVec, o);
-      uint32_t lo = 0, hi = 0;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        lo |= e4m3fn_code(quant_value(o[e], sc)) << (8 * e);
-        hi |= e4m3fn_code(quant_value(o[e + 4], sc)) << (8 * e);
-      }
-      *reinterpret_cast<uint2*>(q + j * kVec) = make_uint2(lo, hi);
-    }
-    tail = nv * kVec;
-  }
-  for (long i = tail + tid; i < n; i += stride)
-    q[i] = (uint8_t)e4m3fn_code(quant_value(widen(Tag{}, x[i]), sc));
-}
-
-int blocks_for(int64_t n) {
-  const int64_t per_block = (int64_t)kThreads * kVec;
-  const int64_t want = (n + per_block - 1) / per_block;
-  return (int)(want < 1 ? 1 : (want > kMaxBlocks ? kMaxBlocks : want));
-}
+using namespace quant;
 
 template <class Tag>
 int launch(const void* xv, int64_t n, uint8_t* q, float* scale, float* partial,

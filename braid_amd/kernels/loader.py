@@ -60,6 +60,9 @@ SIGNATURES = {
                               _vp, _vp, _vp], _i32),
     "braid_quantize_act_workspace": ([_i64], _i32),
     "braid_quantize_act": ([_vp, _i32, _i64, _vp, _vp, _vp, _vp], _i32),
+    "braid_gated_rmsnorm_workspace": ([_i64], _i32),
+    "braid_gated_rmsnorm_quant": ([_vp, _i32, _vp, _i32, _vp, ctypes.c_float, _i64, _i32, _vp,
+                                   _vp, _vp, _vp, _vp], _i32),
 }
 
 
@@ -325,6 +328,43 @@ class GDNKernels:
         self._call("braid_quantize_act", x.device, _ptr(x), _QUANT_DTYPES[x.dtype], n,
                    _ptr(q), _ptr(scale), _ptr(partial))
         return [q, scale]
+
+    # -- gated RMSNorm readout (+ out_proj input quant) -------------------------
+
+    def gated_rmsnorm(self, y: torch.Tensor, z: torch.Tensor, gamma: torch.Tensor,
+                      eps: float, quantize: bool = True):
+        """Readout of the scan (gdn.py:373-387 + norm.py:48-71), fused with the
+        out_proj input quantization (quant.py:209-229).
+
+        y: ``[..., H, HD]`` scan output (fp32, or already z's dtype); z: the gate,
+        same element count, activation dtype; gamma ``[HD]`` fp32. Returns
+        ``core`` shaped like z (z's dtype) and, with ``quantize``, ``q``
+        (float8_e4m3fn, z's shape) and ``scale`` ([1, 1] fp32) as
+        ``quantize_act(core)`` returns them.
+        """
+        _check(y.is_cuda and z.is_cuda and gamma.is_cuda, "y, z and gamma must be cuda")
+        _check(z.dtype in _QUANT_DTYPES, "activation must be fp32, bf16 or fp16")
+        _check(y.dtype in (torch.float32, z.dtype), "y must be fp32 or z's dtype")
+        _check(y.is_contiguous() and z.is_contiguous(), "y and z must be contiguous")
+        _check(gamma.dtype == torch.float32 and gamma.is_contiguous() and gamma.dim() == 1,
+               "gamma must be a contiguous fp32 vector")
+        HD = gamma.numel()
+        _check(HD == 128, "only head_dim=128 is supported")
+        _check(y.numel() == z.numel() and y.numel() % HD == 0,
+               "y and z must hold the same number of head_dim rows")
+        units = y.numel() // HD
+        core = torch.empty(z.shape, dtype=z.dtype, device=z.device)
+        q = scale = partial = None
+        if quantize:
+            _check(units > 0, "x must not be empty")
+            q = torch.empty(z.shape, dtype=torch.float8_e4m3fn, device=z.device)
+            scale = torch.empty((1, 1), dtype=torch.float32, device=z.device)
+            partial = torch.empty(self._lib.braid_gated_rmsnorm_workspace(units),
+                                  dtype=torch.float32, device=z.device)
+        self._call("braid_gated_rmsnorm_quant", z.device, _ptr(y), _QUANT_DTYPES[y.dtype],
+                   _ptr(z), _QUANT_DTYPES[z.dtype], _ptr(gamma), float(eps), units, HD,
+                   _ptr(core), _ptr(q), _ptr(scale), _ptr(partial))
+        return (core, q, scale) if quantize else core
 
 
 @lru_cache(maxsize=1)

@@ -174,6 +174,37 @@ int braid_quantize_act_workspace(int64_t n);
 int braid_quantize_act(const void* x, int x_dtype, int64_t n, uint8_t* q,
                        float* scale, float* partial, void* stream);
 
+/*
+ * Number of fp32 partials braid_gated_rmsnorm_quant needs as workspace for
+ * `units` (token, head) units.
+ */
+int braid_gated_rmsnorm_workspace(int64_t units);
+
+/*
+ * Gated RMSNorm readout of the mixer, optionally fused with the out_proj
+ * input's dynamic FP8 quantization. Replaces the torch readout
+ * GatedDeltaNet._readout + rms_norm_gated (braid/model/gdn.py:373-387,
+ * braid/model/norm.py:48-71) followed by quantize_act (quant.py:209-229) on
+ * its result.
+ *
+ *   y      [units, HD] of y_dtype (BRAID_F32, or act_dtype), dense: the scan
+ *          output, units = tokens * H
+ *   z      [units, HD] of act_dtype (F32, F16 or BF16), dense: the gate
+ *   gamma  [HD] fp32 (stored directly, no unit offset)
+ *   core   [units, HD] of act_dtype, written:
+ *            c = round_act(y); xf = c * rsqrt(mean(c^2) + eps)
+ *            core = round_act(gamma * round_act(xf) * silu(z))
+ *   q, scale, partial: NULL for the norm alone (one launch); else q
+ *          [units*HD] e4m3fn codes and scale [1] fp32 = quantize_act(core)
+ *          bit for bit, with braid_gated_rmsnorm_workspace(units) partials.
+ * HD must be 128; y, z, gamma and core 16-byte aligned. units == 0 is a no-op
+ * for the norm alone and an error with q (quantize_act rejects empty input).
+ */
+int braid_gated_rmsnorm_quant(const void* y, int y_dtype, const void* z,
+                              int act_dtype, const float* gamma, float eps,
+                              int64_t units, int HD, void* core, uint8_t* q,
+                              float* scale, float* partial, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -24,8 +24,8 @@ Pinning (what checks this oracle, in tests/test_oracle.py): brute-force
 float64 Python loops on tiny shapes, a float64 numpy closed form at full
 shape, the reference's own invariants (beta=0 is pure decay, rows
 independent, grouped head->group map, pad identity, chunk split), the
-softplus threshold probes, torch's CPU spelling of the gates and of the
-fp8 cast, and exhaustive e4m3fn round-trips.
+softplus threshold probes, torch's CPU spelling of the gates, of the
+gated RMSNorm readout and of the fp8 cast, and exhaustive e4m3fn round-trips.
 """
 from __future__ import annotations
 
@@ -208,6 +208,39 @@ def conv1d_prefill(conv_pool: np.ndarray, slot_idx, x, weight, bias, seq_lens=No
         for t in range(n):
             out[b, t] = conv1d_decode(conv_pool, idx[b:b + 1], x[b:b + 1, t], weight, bias)[0]
     return out
+
+
+# ---- gated RMSNorm readout ------------------------------------------------------
+
+def gated_rmsnorm(y: np.ndarray, z: np.ndarray, gamma: np.ndarray, eps: float,
+                  act: str) -> np.ndarray:
+    """Readout of the scan, restating braid/model/gdn.py:373-387 (`_readout`:
+    ``y.to(dtype)``) and braid/model/norm.py:48-71 (`rms_norm_gated`):
+
+        c    = round_act(y)
+        xf   = c * rsqrt(mean(c^2) + eps)         over the last axis (HD)
+        h    = gamma * round_act(xf)               fp32 (gamma is fp32)
+        core = round_act(h * (zf / (1 + exp(-zf))))
+
+    y: fp32 values [..., HD]; z: the gate in act storage (uint16 bf16 bits,
+    float16, or float32); gamma [HD] fp32. Returns core in act storage. The
+    mean of squares is summed in float64 and rounded once to fp32, and the
+    reciprocal square root of the fp32 sum ``mean + eps`` is correctly rounded
+    (torch's fp32 reduction and rsqrt differ from these only in rounding).
+    Every other step is one fp32 operation, rounded as torch does.
+    """
+    c = widen(narrow(y, act), act)
+    ms = np.square(c.astype(np.float64)).mean(axis=-1, keepdims=True)
+    t = (ms.astype(np.float32) + np.float32(eps)).astype(np.float32)
+    r = (1.0 / np.sqrt(t.astype(np.float64))).astype(np.float32)
+    xf = (c * r).astype(np.float32)
+    xb = widen(narrow(xf, act), act)
+    h = (np.asarray(gamma, dtype=np.float32) * xb).astype(np.float32)
+    zf = widen(z, act)
+    with np.errstate(over="ignore"):
+        s = (zf / (np.float32(1.0) + np.exp(-zf))).astype(np.float32)
+    o = (h * s).astype(np.float32)
+    return narrow(o, act)
 
 
 # ---- FP8 ---------------------------------------------------------------------

@@ -11,6 +11,8 @@ from __future__ import annotations
 import math
 
 import numpy as np
+import torch
+import torch.nn.functional as F
 
 L2_EPS = 1e-6
 
@@ -93,3 +95,62 @@ def e4m3_table() -> np.ndarray:
         e, m = code >> 3, code & 7
         vals.append(m * 2.0 ** -9 if e == 0 else (1 + m / 8) * 2.0 ** (e - 7))
     return np.array(vals)
+
+
+def torch_gated_readout(y, z, gamma, eps, dtype):
+    """The reference's readout restated in torch (CPU): braid/model/gdn.py:383-386
+    casts the scan output to the activation dtype, then braid/model/norm.py:67-71
+    normalises in fp32, rounds, applies gamma, gates with silu(z) in fp32 and
+    rounds again."""
+    x = (torch.from_numpy(y) if isinstance(y, np.ndarray) else y).to(dtype)
+    g = torch.from_numpy(gamma) if isinstance(gamma, np.ndarray) else gamma
+    gate = z
+    xf = F.rms_norm(x.float(), (x.shape[-1],), None, eps)
+    h = g.to(xf.device) * xf.to(dtype)
+    h = h * F.silu(gate.float())
+    return h.to(dtype)
+
+
+ACT_DTYPES = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
+
+
+def act_storage(t: torch.Tensor, act: str) -> np.ndarray:
+    """Host copy of an act-dtype tensor in the oracle's storage convention."""
+    t = t.detach().cpu()
+    if act == "bf16":
+        return t.view(torch.uint16).numpy()
+    return t.numpy()
+
+
+def act_ulps(a_bits, b_bits, act):
+    """Distance in units in the last place between two arrays in act storage."""
+    if act == "f32":
+        ai = np.asarray(a_bits, np.float32).view(np.int32).astype(np.int64)
+        bi = np.asarray(b_bits, np.float32).view(np.int32).astype(np.int64)
+    else:
+        ai = np.asarray(a_bits).view(np.int16).astype(np.int64)
+        bi = np.asarray(b_bits).view(np.int16).astype(np.int64)
+    # sign-magnitude -> ordered integers
+    bits = 31 if act == "f32" else 15
+    ai = np.where(ai < 0, -(ai & ((1 << bits) - 1)), ai)
+    bi = np.where(bi < 0, -(bi & ((1 << bits) - 1)), bi)
+    return np.abs(ai - bi)
+
+
+# Tolerance of the gated readout against torch's spelling or the oracle, in
+# ulps of the act dtype. The two differ only in the fp32 rounding of the
+# reduction and rsqrt (and the last bits of exp); for 16-bit activations that
+# can flip the rounding of xf.to(act), a change of up to 2^-7 relative, which
+# moves the exact output by up to two of its own ulps before its rounding
+# (three after it). Such flips are rare, so at least 99.5% of elements must be
+# bit-identical. fp32 activations have no intermediate rounding: 8 ulps, 1e-6
+# relative.
+READOUT_ULPS = {"bf16": 3, "f16": 3, "f32": 8}
+
+
+def check_readout(got_bits, ref_bits, act, label=""):
+    u = act_ulps(got_bits, ref_bits, act)
+    assert u.max() <= READOUT_ULPS[act], (label, int(u.max()))
+    if act != "f32":
+        assert (u == 0).mean() >= 0.995, (label, float((u == 0).mean()))
+        assert (u > 1).mean() <= 1e-4, (label, float((u > 1).mean()))

@@ -21,7 +21,8 @@ import torch.nn.functional as F
 
 import oracle
 from braid_amd.config import GDNConfig
-from refmath import conv_f64, decode_f64, decode_naive, e4m3_table, gates_f64
+from refmath import (ACT_DTYPES, act_storage, check_readout, conv_f64, decode_f64, decode_naive,
+                     e4m3_table, gates_f64, torch_gated_readout)
 
 GOLDEN = Path(__file__).resolve().parent / "golden"
 
@@ -335,3 +336,53 @@ def test_conv_prefill_matches_the_reference_torch_spelling():
         np.testing.assert_allclose(out[b, :lens[b]], ref_out[b, :lens[b]], rtol=1e-5, atol=1e-6)
         assert (out[b, lens[b]:] == 0).all()
         np.testing.assert_array_equal(got_pool[slots[b]], keep[b].numpy())
+
+
+# ---- gated RMSNorm readout ---------------------------------------------------
+
+@pytest.mark.parametrize("act", ["bf16", "f16", "f32"])
+def test_gated_rmsnorm_matches_torch_cpu_spelling(act):
+    """Pins oracle.gated_rmsnorm to torch's own spelling of the readout: a
+    dropped intermediate rounding, gamma applied before the cast, a sum
+    instead of a mean or a sigmoid instead of silu moves far more than the
+    handful of one-ulp ties that a different fp32 reduction order can flip."""
+    rng = np.random.default_rng(21)
+    N, H, HD = 48, 32, 128
+    y = (rng.standard_normal((N, H, HD)) * 0.05).astype(np.float32)
+    gamma = (1.0 + 0.3 * rng.standard_normal(HD)).astype(np.float32)
+    zt = torch.from_numpy((rng.standard_normal((N, H, HD)) * 2).astype(np.float32)).to(ACT_DTYPES[act])
+    eps = 1e-6
+    ref = act_storage(torch_gated_readout(y, zt, gamma, eps, ACT_DTYPES[act]), act)
+    got = oracle.gated_rmsnorm(y, act_storage(zt, act), gamma, eps, act)
+    check_readout(got, ref, act)
+
+
+def test_gated_rmsnorm_known_answer_one_hot_row():
+    """y = [2, 0, ..., 0]: mean(c^2) = 4/128, so xf[0] = 2 * sqrt(32) = 11.3137
+    -> bf16 11.3125; with gamma = 1 and z = 30 (silu(30) == 30 in fp32) the
+    output is 339.375 -> bf16 340; every other element is exactly 0."""
+    y = np.zeros((1, 128), np.float32)
+    y[0, 0] = 2.0
+    z = oracle.narrow(np.full((1, 128), 30.0, np.float32), "bf16")
+    core = oracle.widen(oracle.gated_rmsnorm(y, z, np.ones(128, np.float32), 0.0, "bf16"), "bf16")
+    assert core[0, 0] == np.float32(340.0)
+    assert (core[0, 1:] == 0).all()
+
+
+def test_gated_rmsnorm_scale_invariance_and_gate_limits():
+    """With eps = 0 the norm is exactly invariant under a power-of-two scale
+    of y (every rounding scales with it); silu(0) = 0 zeroes a unit; a
+    negative gate flips the sign relative to silu's own sign."""
+    rng = np.random.default_rng(22)
+    y = rng.standard_normal((16, 128)).astype(np.float32)
+    z = oracle.narrow(rng.standard_normal((16, 128)).astype(np.float32), "bf16")
+    gamma = rng.uniform(0.5, 1.5, 128).astype(np.float32)
+    a = oracle.gated_rmsnorm(y, z, gamma, 0.0, "bf16")
+    b = oracle.gated_rmsnorm(y * np.float32(64.0), z, gamma, 0.0, "bf16")
+    assert np.array_equal(a, b)
+    zero = oracle.narrow(np.zeros((16, 128), np.float32), "bf16")
+    assert (oracle.widen(oracle.gated_rmsnorm(y, zero, gamma, 1e-6, "bf16"), "bf16") == 0).all()
+    core = oracle.widen(a, "bf16")
+    zf = oracle.widen(z, "bf16")
+    nz = core != 0
+    assert (np.sign(core[nz]) == np.sign(y[nz] * zf[nz])).all()
