@@ -183,3 +183,52 @@ def test_prefill_rejects_duplicate_slots(kern):
     with pytest.raises(RuntimeError, match="duplicate|distinct"):
         kern.gdn_prefill(p, torch.tensor([1, 1], dtype=torch.int32, device=DEV), inp["q"],
                          inp["k"], inp["v"], inp["alpha"], inp["beta"], y)
+
+
+def _same_up_to_zero_sign(a, b, dt):
+    """Bitwise equal, except that -0 on one side may be +0 on the other."""
+    ib = (lambda t: t.view(torch.int32)) if dt == torch.float32 else (lambda t: t.view(torch.int16))
+    diff = ib(a) != ib(b)
+    return bool((~diff | ((a == 0) & (b == 0))).all())
+
+
+@pytest.mark.parametrize("dt", POOL_DTYPES, ids=POOL_IDS)
+def test_identity_steps_are_exact_up_to_the_sign_of_zero(kern, dt):
+    """alpha = 1, beta = 0 (a pad step) leaves every state element's bits alone
+    except that 1*(-0) + 0 = +0: the reference's own arithmetic
+    (gdn_decode.cu:120-124, S' = a*S + k*delta), whose tests compare with
+    torch.equal, where -0 == +0. Checked with negative zeros planted in the
+    pool, for a caller-padded chunk, a single decode step and a ragged raw-gates
+    chunk against decode over the live tokens only."""
+    B, T = 2, 6
+    p0 = pool(4, dtype=dt, seed=21)
+    p0.view(-1)[::7] = -0.0
+    slots = torch.tensor([3, 1], dtype=torch.int32, device=DEV)
+
+    inp = prefill_inputs(B, T, seed=22)
+    inp["alpha"].fill_(1.0)
+    inp["beta"].zero_()
+    p = p0.clone()
+    y = torch.empty(B, T, 8, 128, device=DEV)
+    kern.gdn_prefill(p, slots, inp["q"], inp["k"], inp["v"], inp["alpha"], inp["beta"], y)
+    assert torch.equal(p, p0) and _same_up_to_zero_sign(p, p0, dt)
+
+    p = p0.clone()
+    out = torch.empty(B, 8, 128, device=DEV)
+    kern.gdn_decode(p, slots, inp["q"][:, 0].contiguous(), inp["k"][:, 0].contiguous(),
+                    inp["v"][:, 0].contiguous(), inp["alpha"][:, 0].contiguous(),
+                    inp["beta"][:, 0].contiguous(), out)
+    assert torch.equal(p, p0) and _same_up_to_zero_sign(p, p0, dt)
+
+    a_raw, b_raw, A, dt_bias = raw_gates((B, T, 8), 8, torch.bfloat16, seed=23)
+    lens = torch.tensor([2, 0], dtype=torch.int32, device=DEV)
+    pr = p0.clone()
+    kern.gdn_prefill_raw(pr, slots, inp["q"], inp["k"], inp["v"], a_raw, b_raw, A, dt_bias, y,
+                         lens)
+    pd = p0.clone()
+    for t in range(2):
+        o = torch.empty(1, 8, 128, device=DEV)
+        kern.gdn_decode_raw(pd, slots[:1], inp["q"][:1, t].contiguous(),
+                            inp["k"][:1, t].contiguous(), inp["v"][:1, t].contiguous(),
+                            a_raw[:1, t].contiguous(), b_raw[:1, t].contiguous(), A, dt_bias, o)
+    assert torch.equal(pr, pd) and _same_up_to_zero_sign(pr, pd, dt)
