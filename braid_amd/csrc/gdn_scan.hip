@@ -1,12 +1,13 @@
 // Batched Gated DeltaNet decode step and chunk prefill scan for gfx950.
 //
 // Both kernels launch one workgroup per (batch row, value head) tile and run
-// the same per-token device function, braid::gdn_token: decode with four waves
-// of 32 state rows x 128 columns, prefill with eight waves (the same rows,
-// each tile's columns split in two halves), which changes no bit. Decode loads the tile from the slot-indexed pool,
-// runs one token and stores it back; prefill loads it once, runs T tokens with
-// the tile resident in registers (in the pool's storage type) and stores it
-// once. Reference behaviour: braid/kernels/csrc/gdn_decode.cu:156-272 (decode)
+// the same per-token arithmetic with the same summation trees: decode with
+// four waves of 32 state rows x 128 columns (gdn_token, column sums finished
+// across waves in LDS), prefill with eight waves of 128 rows x 16 columns
+// (scan_token, column sums finished inside each wave, no barrier per token).
+// Decode loads the tile from the slot-indexed pool, runs one token and stores
+// it back; prefill loads it once, runs T tokens with the tile resident in
+// registers (in the pool's storage type) and stores it once. Reference behaviour: braid/kernels/csrc/gdn_decode.cu:156-272 (decode)
 // and :467-551 (prefill); entry-point contracts :313-441 and :553-699.
 #include "capi_common.h"
 #include "gdn_tile.h"
@@ -64,76 +65,100 @@ gdn_decode_kernel(typename Storage<Tag>::T* __restrict__ pool, const int* __rest
   if (L.stores_y()) storeN<CPL>(y + ((size_t)b * H + h) * kHD + L.col0, yy);
 }
 
-// Per-token values of a prefill chunk that do not depend on the state.
-constexpr int kScanChunk = 256;
-struct ChunkLds {
-  float gate[kScanChunk][2];  // alpha, beta
-  float inv[kScanChunk][2];   // 1/|q|, 1/|k| (with the 1e-6 epsilon)
+// A prefill stage: the next kStage tokens' per-token inputs, staged in LDS by
+// a parallel prologue so that the serial loop reads nothing from global memory
+// but its outputs' addresses:
+//   qk   normalised q and k (q_hat, k_hat), each [kSS] in the lane order of the
+//        scan layout: the eight rows w * 32 + rg + 4 i of lane (w, rg) sit at
+//        ((w * 4 + rg) * 8 + i), two 16-byte reads per vector;
+//   v    the value row [kHD];
+//   gate alpha, beta.
+constexpr int kStage = 32;
+struct StageLds {
+  float qk[kStage][2][kSS];
+  float v[kStage][kHD];
+  float gate[kStage][2];
 };
 
-// Fills `cl` for tokens [t0, t0 + n) of row b, head h: every thread evaluates
-// one token's gates (the policy's own arithmetic, as publish_gates runs it),
-// and each wave computes the q/k norm factors of every (waves)-th token with
-// the same 64-lane butterfly as the decode kernel's normalize_qk, two tokens at
-// a time so the two shuffle chains overlap. Same values, same bits.
-template <class Gates, int CPL>
-__device__ __forceinline__ void scan_chunk_prologue(const LaneMap<CPL>& L, const Gates& gates,
+__device__ __forceinline__ int scan_order(int r) {
+  return ((r >> 5) * kRowGroups + (r & 3)) * kRowsPerLane + ((r & 31) >> 2);
+}
+
+// Fills `st` for tokens [t0, t0 + n) of row b, head h. Gates: one thread per
+// token, the policy's own arithmetic. q and k: each wave takes every
+// (waves)-th token, two at a time so the butterflies overlap, and computes the
+// norm factor with the decode's butterfly (inv_norm) and q_hat = q * factor as
+// decode's scale_qk does: the same bits. v: 16-byte copies.
+template <int kTileWaves, class Gates>
+__device__ __forceinline__ void scan_stage_prologue(int wave, int lane, const Gates& gates,
                                                     const float* __restrict__ q,
-                                                    const float* __restrict__ k, int b, int h,
+                                                    const float* __restrict__ k,
+                                                    const float* __restrict__ v, int b, int h,
                                                     int g, int H, int G, int T, int t0, int n,
-                                                    ChunkLds& cl) {
-  constexpr int kThreads = tile_threads(CPL);
-  constexpr int kTileWaves = kThreads / 64;
+                                                    StageLds& st) {
+  constexpr int kThreads = 64 * kTileWaves;
   for (int j = threadIdx.x; j < n; j += kThreads) {
     const GateRaw r = gates.load(b, h, t0 + j, H, T);
-    cl.gate[j][0] = gates.eval_alpha(r, h);
-    cl.gate[j][1] = gates.eval_beta(r);
+    st.gate[j][0] = gates.eval_alpha(r, h);
+    st.gate[j][1] = gates.eval_beta(r);
   }
-  for (int j = L.wave; j < n; j += 2 * kTileWaves) {
+  constexpr int kV4 = kHD / 4;
+  for (int e = threadIdx.x; e < n * kV4; e += kThreads) {
+    const int j = e / kV4, c4 = e % kV4;
+    *reinterpret_cast<float4*>(&st.v[j][4 * c4]) =
+        *reinterpret_cast<const float4*>(v + (((size_t)b * T + t0 + j) * H + h) * kHD + 4 * c4);
+  }
+  const int p0 = scan_order(2 * lane), p1 = scan_order(2 * lane + 1);
+  for (int j = wave; j < n; j += 2 * kTileWaves) {
     const int j2 = j + kTileWaves;
-    const size_t o1 = (((size_t)b * T + t0 + j) * G + g) * kSS + 2 * L.lane;
+    const size_t o1 = (((size_t)b * T + t0 + j) * G + g) * kSS + 2 * lane;
     const float2 q1 = *reinterpret_cast<const float2*>(q + o1);
     const float2 k1 = *reinterpret_cast<const float2*>(k + o1);
     float2 q2 = make_float2(0.f, 0.f), k2 = make_float2(0.f, 0.f);
     if (j2 < n) {
-      const size_t o2 = (((size_t)b * T + t0 + j2) * G + g) * kSS + 2 * L.lane;
+      const size_t o2 = (((size_t)b * T + t0 + j2) * G + g) * kSS + 2 * lane;
       q2 = *reinterpret_cast<const float2*>(q + o2);
       k2 = *reinterpret_cast<const float2*>(k + o2);
     }
     const float qi1 = inv_norm(q1), ki1 = inv_norm(k1);
     const float qi2 = inv_norm(q2), ki2 = inv_norm(k2);
-    if (L.lane == 0) {
-      cl.inv[j][0] = qi1;
-      cl.inv[j][1] = ki1;
-      if (j2 < n) {
-        cl.inv[j2][0] = qi2;
-        cl.inv[j2][1] = ki2;
-      }
+    st.qk[j][0][p0] = q1.x * qi1;
+    st.qk[j][0][p1] = q1.y * qi1;
+    st.qk[j][1][p0] = k1.x * ki1;
+    st.qk[j][1][p1] = k1.y * ki1;
+    if (j2 < n) {
+      st.qk[j2][0][p0] = q2.x * qi2;
+      st.qk[j2][0][p1] = q2.y * qi2;
+      st.qk[j2][1][p0] = k2.x * ki2;
+      st.qk[j2][1][p1] = k2.y * ki2;
     }
   }
 }
 
-// T tokens for the tile with the state resident in registers, in the column-
-// split layout (4 columns per lane, eight waves): the same per-column
-// arithmetic as the decode kernel, token by token. Tokens are processed in
-// chunks of kScanChunk: a parallel prologue computes the chunk's gates and q/k
-// norm factors into LDS, so the serial loop carries only the recurrence.
+// T tokens for the tile with the state resident in registers. Scan layout
+// (WaveColMap): each of the eight waves owns 16 whole columns, so the serial
+// loop has no workgroup barrier; the column sums are VALU butterflies with the
+// decode's summation tree, so the bits are the decode's. Tokens run in stages
+// of kStage: a parallel prologue stages their inputs in LDS (StageLds), then
+// the serial loop carries only the recurrence and the output stores.
 template <class Tag, class Gates>
-__global__ void __launch_bounds__(tile_threads(kPrefillCols))
+__global__ void __launch_bounds__(64 * WaveColMap<kPrefillCols>::kWavesPerTile)
 gdn_prefill_kernel(typename Storage<Tag>::T* __restrict__ pool,
                    const int* __restrict__ slot_idx,
                    const float* __restrict__ q, const float* __restrict__ k,
                    const float* __restrict__ v, Gates gates, float* __restrict__ y,
                    int H, int G, int heads_per_group, int T) {
   constexpr int CPL = kPrefillCols;
+  static_assert(CPL == 4, "the staged v row is read as one 16-byte vector per lane");
+  using LM = WaveColMap<CPL>;
   using ST = typename Storage<Tag>::T;
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
   const int b = blockIdx.x / H;
   const int h = blockIdx.x - b * H;
   const int g = h / heads_per_group;
-  const LaneMap<CPL> L(threadIdx.x);
+  const LM L(threadIdx.x);
 
-  __shared__ TileLds lds;
-  __shared__ ChunkLds cl;
+  __shared__ StageLds st;
   const int slot = slot_idx[b];
   ST* tile = pool + ((size_t)slot * H + h) * (kSS * kHD) + L.col0;
 
@@ -141,39 +166,36 @@ gdn_prefill_kernel(typename Storage<Tag>::T* __restrict__ pool,
 #pragma unroll
   for (int i = 0; i < kRowsPerLane; ++i) S[i].load_nt(tile + (size_t)L.row(i) * kHD);
 
-  for (int t0 = 0; t0 < T; t0 += kScanChunk) {
-    const int n = min(kScanChunk, T - t0);
-    // The previous chunk's last token ended with a barrier after its last LDS
-    // reads, so the prologue may overwrite `cl`; this barrier publishes it.
-    scan_chunk_prologue(L, gates, q, k, b, h, g, H, G, T, t0, n, cl);
+  const int qk_off = (L.w * kRowGroups + L.rg) * kRowsPerLane;
+  for (int t0 = 0; t0 < T; t0 += kStage) {
+    const int n = min(kStage, T - t0);
+    // Every wave has finished reading the previous stage (the barrier at the
+    // end of the stage loop), so the prologue may overwrite it.
+    scan_stage_prologue<LM::kWavesPerTile>(L.wave, L.lane, gates, q, k, v, b, h, g, H, G, T, t0,
+                                           n, st);
     __syncthreads();
-
-    // Inputs of token t + 1 are loaded while token t runs.
-    QKRaw raw;
-    float vv[CPL];
-    load_qk(L, q + (((size_t)b * T + t0) * G + g) * kSS, k + (((size_t)b * T + t0) * G + g) * kSS,
-            raw);
-    loadN<CPL>(v + (((size_t)b * T + t0) * H + h) * kHD + L.col0, vv);
     for (int j = 0; j < n; ++j) {
-      const size_t bt_idx = (size_t)b * T + t0 + j;
-      const bool more = j + 1 < n;
-      QKRaw raw_n;
-      float vv_n[CPL];
-      if (more) {
-        load_qk(L, q + ((bt_idx + 1) * G + g) * kSS, k + ((bt_idx + 1) * G + g) * kSS, raw_n);
-        loadN<CPL>(v + ((bt_idx + 1) * H + h) * kHD + L.col0, vv_n);
-      }
       QK qk;
-      scale_qk(raw, cl.inv[j][0], cl.inv[j][1], qk);
-      float yy[CPL];
-      gdn_token<Tag, CPL>(L, S, qk, vv, lds, cl.gate[j], yy);
-      if (L.stores_y()) storeN<CPL>(y + (bt_idx * H + h) * kHD + L.col0, yy);
-      if (more) {
-        raw = raw_n;
+      const f32x4 q0 = *reinterpret_cast<const f32x4*>(&st.qk[j][0][qk_off]);
+      const f32x4 q1 = *reinterpret_cast<const f32x4*>(&st.qk[j][0][qk_off + 4]);
+      const f32x4 k0 = *reinterpret_cast<const f32x4*>(&st.qk[j][1][qk_off]);
+      const f32x4 k1 = *reinterpret_cast<const f32x4*>(&st.qk[j][1][qk_off + 4]);
 #pragma unroll
-        for (int c = 0; c < CPL; ++c) vv[c] = vv_n[c];
+      for (int i = 0; i < 4; ++i) {
+        qk.qh[i] = q0[i];
+        qk.qh[i + 4] = q1[i];
+        qk.kh[i] = k0[i];
+        qk.kh[i + 4] = k1[i];
       }
+      float vv[CPL];
+      const f32x4 v4 = *reinterpret_cast<const f32x4*>(&st.v[j][L.col0]);
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) vv[c] = v4[c];
+      float yy[CPL];
+      scan_token<Tag, CPL>(S, qk, vv, st.gate[j][0], st.gate[j][1], yy);
+      if (L.stores_y()) storeN<CPL>(y + (((size_t)b * T + t0 + j) * H + h) * kHD + L.col0, yy);
     }
+    __syncthreads();
   }
 
 #pragma unroll
@@ -246,7 +268,7 @@ template <class Gates>
 int launch_prefill(void* pool, int pool_dtype, const int32_t* slot_idx, int B, int T, int H,
                    int G, const float* q, const float* k, const float* v, Gates gates,
                    float* y, hipStream_t stream) {
-  const dim3 grid((unsigned)B * (unsigned)H), block(tile_threads(kPrefillCols));
+  const dim3 grid((unsigned)B * (unsigned)H), block(64 * WaveColMap<kPrefillCols>::kWavesPerTile);
   const int hpg = H / G;
   switch (pool_dtype) {
     case BRAID_F32:

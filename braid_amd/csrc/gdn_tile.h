@@ -285,6 +285,62 @@ struct LaneMap {
   __device__ __forceinline__ bool stores_y() const { return rg == 0 && cc / 4 == w; }
 };
 
+// Lane geometry of the scan (prefill) layout: every wave owns whole columns,
+// all 128 rows of them, so a column sum never leaves the wave and a token
+// needs no workgroup barrier. Lane bits: 0-1 row group rg, 2-3 column chunk
+// cc, 4-5 row block w. A lane holds the same rows as in the decode layout,
+// w * 32 + rg + 4 i, so its in-lane chain is the decode chain; the cross-lane
+// tree (rg pairs, then rg pairs of pairs, then (w0 + w1) + (w2 + w3)) is the
+// decode tree too, so every sum has the decode's bits.
+template <int CPL>
+struct WaveColMap {
+  static constexpr int kColsPerWave = 4 * CPL;
+  static constexpr int kWavesPerTile = kHD / kColsPerWave;
+  int wave, lane, rg, cc, w, col0;
+  __device__ __forceinline__ WaveColMap(int tid) {
+    lane = tid & 63;
+    wave = tid >> 6;
+    rg = lane & 3;
+    cc = (lane >> 2) & 3;
+    w = lane >> 4;
+    col0 = wave * kColsPerWave + cc * CPL;
+  }
+  __device__ __forceinline__ int row(int i) const {
+    return w * kRowsPerWave + rg + kRowGroups * i;
+  }
+  // One lane per column chunk holds (like all others) the totals and writes them.
+  __device__ __forceinline__ bool stores_y() const { return rg == 0 && w == 0; }
+};
+
+// Partner exchanges of the scan layout's tree, all VALU (no LDS):
+// lane xor 1 and xor 2 through DPP quad permutations, xor 16 and xor 32
+// through gfx950's v_permlane16_swap / v_permlane32_swap. Each stage adds the
+// two partners' values, which is the same sum in both partners.
+__device__ __forceinline__ float add_xor1(float v) {
+  return v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float add_xor2(float v) {
+  return v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));
+}
+// After the swap of v with itself, the two results hold the even and the odd
+// row's (lane block's) value in every lane, so their sum is the pair's sum.
+__device__ __forceinline__ float add_xor16(float v) {
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+__device__ __forceinline__ float add_xor32(float v) {
+  const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+
+// Column total of the scan layout from each lane's in-lane chain value:
+// ((rg0 + rg1) + (rg2 + rg3)) per row block, then (w0 + w1) + (w2 + w3).
+__device__ __forceinline__ float scan_column_sum(float v) {
+  return add_xor32(add_xor16(add_xor2(add_xor1(v))));
+}
+
 // Cross-wave exchange buffers for one tile: per-row-block column partials of
 // kv and of y, kept apart so one token's y exchange never overwrites kv
 // partials a slower wave is still reading (and vice versa across tokens).
@@ -444,6 +500,22 @@ __device__ __forceinline__ void gdn_token(const LaneMap<CPL>& L,
   column_sums_take<CPL>(L, acc, lds.y);
 #pragma unroll
   for (int c = 0; c < CPL; ++c) y[c] = acc[c] * kYScale;
+}
+
+// One token of the scan on this lane's 8 x CPL block, in the scan layout:
+// the decode token's arithmetic with the column sums done inside the wave.
+template <class Tag, int CPL>
+__device__ __forceinline__ void scan_token(Row<Tag, CPL> (&S)[kRowsPerLane], const QK& qk,
+                                           const float (&v)[CPL], float alpha, float beta,
+                                           float (&y)[CPL]) {
+  float kv[CPL];
+  kv_partials<Tag, CPL>(S, qk, kv);
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) kv[c] = scan_column_sum(kv[c]);
+  float acc[CPL];
+  update_state<Tag, CPL>(S, qk, v, kv, alpha, beta, acc);
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) y[c] = scan_column_sum(acc[c]) * kYScale;
 }
 
 // Computes one token's gates ONCE per tile and leaves them in lds.gate for
