@@ -3,7 +3,7 @@
 // Both kernels launch one workgroup per (batch row, value head) tile and run
 // the same per-token arithmetic with the same summation trees: decode with
 // four waves of 32 state rows x 128 columns (gdn_token, column sums finished
-// across waves in LDS), prefill with eight waves of 128 rows x 16 columns
+// across waves in LDS), prefill with four waves of 128 rows x 32 columns
 // (scan_token, column sums finished inside each wave, no barrier per token).
 // Decode loads the tile from the slot-indexed pool, runs one token and stores
 // it back; prefill loads it once, runs T tokens with the tile resident in
@@ -66,11 +66,8 @@ gdn_decode_kernel(typename Storage<Tag>::T* __restrict__ pool, const int* __rest
 }
 
 // A prefill stage: the next kStage tokens' per-token inputs, staged in LDS by
-// a parallel prologue so that the serial loop reads nothing from global memory
-// but its outputs' addresses:
-//   qk   normalised q and k (q_hat, k_hat), each [kSS] in the lane order of the
-//        scan layout: the eight rows w * 32 + rg + 4 i of lane (w, rg) sit at
-//        ((w * 4 + rg) * 8 + i), two 16-byte reads per vector;
+// a parallel prologue so that the serial loop reads nothing from global memory:
+//   qk   normalised q and k (q_hat, k_hat), each [kSS] in row order;
 //   v    the value row [kHD];
 //   gate alpha, beta.
 constexpr int kStage = 32;
@@ -79,10 +76,6 @@ struct StageLds {
   float v[kStage][kHD];
   float gate[kStage][2];
 };
-
-__device__ __forceinline__ int scan_order(int r) {
-  return ((r >> 5) * kRowGroups + (r & 3)) * kRowsPerLane + ((r & 31) >> 2);
-}
 
 // Fills `st` for tokens [t0, t0 + n) of row b, head h. Gates: one thread per
 // token, the policy's own arithmetic. q and k: each wave takes every
@@ -108,7 +101,6 @@ __device__ __forceinline__ void scan_stage_prologue(int wave, int lane, const Ga
     *reinterpret_cast<float4*>(&st.v[j][4 * c4]) =
         *reinterpret_cast<const float4*>(v + (((size_t)b * T + t0 + j) * H + h) * kHD + 4 * c4);
   }
-  const int p0 = scan_order(2 * lane), p1 = scan_order(2 * lane + 1);
   for (int j = wave; j < n; j += 2 * kTileWaves) {
     const int j2 = j + kTileWaves;
     const size_t o1 = (((size_t)b * T + t0 + j) * G + g) * kSS + 2 * lane;
@@ -122,37 +114,61 @@ __device__ __forceinline__ void scan_stage_prologue(int wave, int lane, const Ga
     }
     const float qi1 = inv_norm(q1), ki1 = inv_norm(k1);
     const float qi2 = inv_norm(q2), ki2 = inv_norm(k2);
-    st.qk[j][0][p0] = q1.x * qi1;
-    st.qk[j][0][p1] = q1.y * qi1;
-    st.qk[j][1][p0] = k1.x * ki1;
-    st.qk[j][1][p1] = k1.y * ki1;
+    *reinterpret_cast<float2*>(&st.qk[j][0][2 * lane]) = make_float2(q1.x * qi1, q1.y * qi1);
+    *reinterpret_cast<float2*>(&st.qk[j][1][2 * lane]) = make_float2(k1.x * ki1, k1.y * ki1);
     if (j2 < n) {
-      st.qk[j2][0][p0] = q2.x * qi2;
-      st.qk[j2][0][p1] = q2.y * qi2;
-      st.qk[j2][1][p0] = k2.x * ki2;
-      st.qk[j2][1][p1] = k2.y * ki2;
+      *reinterpret_cast<float2*>(&st.qk[j2][0][2 * lane]) = make_float2(q2.x * qi2, q2.y * qi2);
+      *reinterpret_cast<float2*>(&st.qk[j2][1][2 * lane]) = make_float2(k2.x * ki2, k2.y * ki2);
     }
   }
 }
 
+// One token's inputs for a lane of the scan layout, read from the stage.
+struct TokenIn {
+  float kh[kRowsPerWave], qh[kRowsPerWave];  // the lane's row block, row order
+  float v[kPrefillCols];
+  float alpha, beta;
+};
+
+__device__ __forceinline__ void read_token(const StageLds& st, int j, int r0, int col0,
+                                           TokenIn& t) {
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+  for (int r = 0; r < kRowsPerWave; r += 4) {
+    const f32x4 k4 = *reinterpret_cast<const f32x4*>(&st.qk[j][1][r0 + r]);
+    const f32x4 q4 = *reinterpret_cast<const f32x4*>(&st.qk[j][0][r0 + r]);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      t.kh[r + e] = k4[e];
+      t.qh[r + e] = q4[e];
+    }
+  }
+  const float2 v2 = *reinterpret_cast<const float2*>(&st.v[j][col0]);
+  t.v[0] = v2.x;
+  t.v[1] = v2.y;
+  t.alpha = st.gate[j][0];
+  t.beta = st.gate[j][1];
+}
+
 // T tokens for the tile with the state resident in registers. Scan layout
-// (WaveColMap): each of the eight waves owns 16 whole columns, so the serial
-// loop has no workgroup barrier; the column sums are VALU butterflies with the
-// decode's summation tree, so the bits are the decode's. Tokens run in stages
-// of kStage: a parallel prologue stages their inputs in LDS (StageLds), then
-// the serial loop carries only the recurrence and the output stores.
+// (ScanMap): four waves, each owning 32 whole columns, a lane holding the 32
+// rows of its row block for two columns; the column sums finish in-lane and
+// over the four row blocks with permlane swaps, by the decode's summation
+// tree, so the bits are the decode's and no token needs a workgroup barrier.
+// Tokens run in stages of kStage: a parallel prologue stages their inputs in
+// LDS (StageLds), then the serial loop carries only the recurrence and the
+// output stores.
 template <class Tag, class Gates>
-__global__ void __launch_bounds__(64 * WaveColMap<kPrefillCols>::kWavesPerTile)
+__global__ void __launch_bounds__(64 * ScanMap<kPrefillCols>::kWavesPerTile)
 gdn_prefill_kernel(typename Storage<Tag>::T* __restrict__ pool,
                    const int* __restrict__ slot_idx,
                    const float* __restrict__ q, const float* __restrict__ k,
                    const float* __restrict__ v, Gates gates, float* __restrict__ y,
                    int H, int G, int heads_per_group, int T) {
   constexpr int CPL = kPrefillCols;
-  static_assert(CPL == 4, "the staged v row is read as one 16-byte vector per lane");
-  using LM = WaveColMap<CPL>;
+  static_assert(CPL == 2, "the staged v entries are read as one 8-byte vector per lane");
+  using LM = ScanMap<CPL>;
   using ST = typename Storage<Tag>::T;
-  typedef float f32x4 __attribute__((ext_vector_type(4)));
   const int b = blockIdx.x / H;
   const int h = blockIdx.x - b * H;
   const int g = h / heads_per_group;
@@ -162,11 +178,14 @@ gdn_prefill_kernel(typename Storage<Tag>::T* __restrict__ pool,
   const int slot = slot_idx[b];
   ST* tile = pool + ((size_t)slot * H + h) * (kSS * kHD) + L.col0;
 
-  Row<Tag, CPL> S[kRowsPerLane];
+  Row<Tag, CPL> S[kRowGroups][kRowsPerLane];
 #pragma unroll
-  for (int i = 0; i < kRowsPerLane; ++i) S[i].load_nt(tile + (size_t)L.row(i) * kHD);
+  for (int rg = 0; rg < kRowGroups; ++rg) {
+#pragma unroll
+    for (int i = 0; i < kRowsPerLane; ++i) S[rg][i].load_nt(tile + (size_t)L.row(rg, i) * kHD);
+  }
 
-  const int qk_off = (L.w * kRowGroups + L.rg) * kRowsPerLane;
+  const int r0 = L.w * kRowsPerWave;
   for (int t0 = 0; t0 < T; t0 += kStage) {
     const int n = min(kStage, T - t0);
     // Every wave has finished reading the previous stage (the barrier at the
@@ -174,32 +193,22 @@ gdn_prefill_kernel(typename Storage<Tag>::T* __restrict__ pool,
     scan_stage_prologue<LM::kWavesPerTile>(L.wave, L.lane, gates, q, k, v, b, h, g, H, G, T, t0,
                                            n, st);
     __syncthreads();
+    // Token j + 1's staged inputs are read while token j computes.
     for (int j = 0; j < n; ++j) {
-      QK qk;
-      const f32x4 q0 = *reinterpret_cast<const f32x4*>(&st.qk[j][0][qk_off]);
-      const f32x4 q1 = *reinterpret_cast<const f32x4*>(&st.qk[j][0][qk_off + 4]);
-      const f32x4 k0 = *reinterpret_cast<const f32x4*>(&st.qk[j][1][qk_off]);
-      const f32x4 k1 = *reinterpret_cast<const f32x4*>(&st.qk[j][1][qk_off + 4]);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        qk.qh[i] = q0[i];
-        qk.qh[i + 4] = q1[i];
-        qk.kh[i] = k0[i];
-        qk.kh[i + 4] = k1[i];
-      }
-      float vv[CPL];
-      const f32x4 v4 = *reinterpret_cast<const f32x4*>(&st.v[j][L.col0]);
-#pragma unroll
-      for (int c = 0; c < CPL; ++c) vv[c] = v4[c];
+      TokenIn in;
+      read_token(st, j, r0, L.col0, in);
       float yy[CPL];
-      scan_token<Tag, CPL>(S, qk, vv, st.gate[j][0], st.gate[j][1], yy);
+      scan_token<Tag, CPL>(S, in.kh, in.qh, in.v, in.alpha, in.beta, yy);
       if (L.stores_y()) storeN<CPL>(y + (((size_t)b * T + t0 + j) * H + h) * kHD + L.col0, yy);
     }
     __syncthreads();
   }
 
 #pragma unroll
-  for (int i = 0; i < kRowsPerLane; ++i) S[i].store_nt(tile + (size_t)L.row(i) * kHD);
+  for (int rg = 0; rg < kRowGroups; ++rg) {
+#pragma unroll
+    for (int i = 0; i < kRowsPerLane; ++i) S[rg][i].store_nt(tile + (size_t)L.row(rg, i) * kHD);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -268,7 +277,7 @@ template <class Gates>
 int launch_prefill(void* pool, int pool_dtype, const int32_t* slot_idx, int B, int T, int H,
                    int G, const float* q, const float* k, const float* v, Gates gates,
                    float* y, hipStream_t stream) {
-  const dim3 grid((unsigned)B * (unsigned)H), block(64 * WaveColMap<kPrefillCols>::kWavesPerTile);
+  const dim3 grid((unsigned)B * (unsigned)H), block(64 * ScanMap<kPrefillCols>::kWavesPerTile);
   const int hpg = H / G;
   switch (pool_dtype) {
     case BRAID_F32:

@@ -66,7 +66,7 @@ constexpr float kYScale = 0.088388347648318440550f;
 // Threads of a tile's workgroup when each lane owns `cpl` columns.
 constexpr int tile_threads(int cpl) { return 64 * kWaves * (8 / cpl); }
 constexpr int kDecodeCols = 8;   // columns per lane, decode
-constexpr int kPrefillCols = 4;  // columns per lane, prefill
+constexpr int kPrefillCols = 2;  // columns per lane, prefill
 
 // ---------------------------------------------------------------------------
 // Storage types. A Row<Tag, N> is the N consecutive elements of one state row
@@ -285,43 +285,37 @@ struct LaneMap {
   __device__ __forceinline__ bool stores_y() const { return rg == 0 && cc / 4 == w; }
 };
 
-// Lane geometry of the scan (prefill) layout: every wave owns whole columns,
-// all 128 rows of them, so a column sum never leaves the wave and a token
-// needs no workgroup barrier. Lane bits: 0-1 row group rg, 2-3 column chunk
-// cc, 4-5 row block w. A lane holds the same rows as in the decode layout,
-// w * 32 + rg + 4 i, so its in-lane chain is the decode chain; the cross-lane
-// tree (rg pairs, then rg pairs of pairs, then (w0 + w1) + (w2 + w3)) is the
-// decode tree too, so every sum has the decode's bits.
+// Lane geometry of the scan (prefill) layout: a lane holds all 32 rows of its
+// row block w for CPL columns, so the row-group level of every column sum is
+// done in-lane and a column sum crosses lanes only over the four row blocks.
+// Lane bits: 0-3 column chunk cc, 4-5 row block w; a wave owns 16 * CPL whole
+// columns, so a token needs no workgroup barrier. The lane's rows are indexed
+// (rg, i) -> w * 32 + rg + 4 i as in the decode layout, so its four in-lane
+// chains are the decode chains of row groups 0..3, combined as
+// (rg0 + rg1) + (rg2 + rg3) like the decode's lane-xor-16 / xor-32 stages, and
+// the row blocks as (w0 + w1) + (w2 + w3) like the decode's LDS tree: every
+// sum has the decode's bits.
 template <int CPL>
-struct WaveColMap {
-  static constexpr int kColsPerWave = 4 * CPL;
+struct ScanMap {
+  static constexpr int kColsPerWave = 16 * CPL;
   static constexpr int kWavesPerTile = kHD / kColsPerWave;
-  int wave, lane, rg, cc, w, col0;
-  __device__ __forceinline__ WaveColMap(int tid) {
+  int wave, lane, cc, w, col0;
+  __device__ __forceinline__ ScanMap(int tid) {
     lane = tid & 63;
     wave = tid >> 6;
-    rg = lane & 3;
-    cc = (lane >> 2) & 3;
+    cc = lane & 15;
     w = lane >> 4;
     col0 = wave * kColsPerWave + cc * CPL;
   }
-  __device__ __forceinline__ int row(int i) const {
+  __device__ __forceinline__ int row(int rg, int i) const {
     return w * kRowsPerWave + rg + kRowGroups * i;
   }
-  // One lane per column chunk holds (like all others) the totals and writes them.
-  __device__ __forceinline__ bool stores_y() const { return rg == 0 && w == 0; }
+  // Row block 0's lanes write the column totals (every lane holds them).
+  __device__ __forceinline__ bool stores_y() const { return w == 0; }
 };
 
-// Partner exchanges of the scan layout's tree, all VALU (no LDS):
-// lane xor 1 and xor 2 through DPP quad permutations, xor 16 and xor 32
-// through gfx950's v_permlane16_swap / v_permlane32_swap. Each stage adds the
-// two partners' values, which is the same sum in both partners.
-__device__ __forceinline__ float add_xor1(float v) {
-  return v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));
-}
-__device__ __forceinline__ float add_xor2(float v) {
-  return v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));
-}
+// Partner exchanges of the scan layout's tree, all VALU (no LDS): lane
+// xor 16 and xor 32 through gfx950's v_permlane16_swap / v_permlane32_swap.
 // After the swap of v with itself, the two results hold the even and the odd
 // row's (lane block's) value in every lane, so their sum is the pair's sum.
 __device__ __forceinline__ float add_xor16(float v) {
@@ -335,10 +329,10 @@ __device__ __forceinline__ float add_xor32(float v) {
   return __uint_as_float(p[0]) + __uint_as_float(p[1]);
 }
 
-// Column total of the scan layout from each lane's in-lane chain value:
-// ((rg0 + rg1) + (rg2 + rg3)) per row block, then (w0 + w1) + (w2 + w3).
-__device__ __forceinline__ float scan_column_sum(float v) {
-  return add_xor32(add_xor16(add_xor2(add_xor1(v))));
+// Column total of the scan layout from a lane's four row-group chains:
+// (rg0 + rg1) + (rg2 + rg3) in-lane, then (w0 + w1) + (w2 + w3) across lanes.
+__device__ __forceinline__ float scan_column_sum(float c0, float c1, float c2, float c3) {
+  return add_xor32(add_xor16((c0 + c1) + (c2 + c3)));
 }
 
 // Cross-wave exchange buffers for one tile: per-row-block column partials of
@@ -502,20 +496,53 @@ __device__ __forceinline__ void gdn_token(const LaneMap<CPL>& L,
   for (int c = 0; c < CPL; ++c) y[c] = acc[c] * kYScale;
 }
 
-// One token of the scan on this lane's 8 x CPL block, in the scan layout:
-// the decode token's arithmetic with the column sums done inside the wave.
+// One token of the scan on this lane's 32 x CPL block (S[rg][i] = row
+// w * 32 + rg + 4 i), in the scan layout: the decode token's arithmetic, each
+// element's operations in the decode's order. kh / qh hold the row block's 32
+// normalised key / query entries in row order.
 template <class Tag, int CPL>
-__device__ __forceinline__ void scan_token(Row<Tag, CPL> (&S)[kRowsPerLane], const QK& qk,
+__device__ __forceinline__ void scan_token(Row<Tag, CPL> (&S)[kRowGroups][kRowsPerLane],
+                                           const float (&kh)[kRowsPerWave],
+                                           const float (&qh)[kRowsPerWave],
                                            const float (&v)[CPL], float alpha, float beta,
                                            float (&y)[CPL]) {
-  float kv[CPL];
-  kv_partials<Tag, CPL>(S, qk, kv);
+  float ch[kRowGroups][CPL];
 #pragma unroll
-  for (int c = 0; c < CPL; ++c) kv[c] = scan_column_sum(kv[c]);
-  float acc[CPL];
-  update_state<Tag, CPL>(S, qk, v, kv, alpha, beta, acc);
+  for (int rg = 0; rg < kRowGroups; ++rg) {
 #pragma unroll
-  for (int c = 0; c < CPL; ++c) y[c] = scan_column_sum(acc[c]) * kYScale;
+    for (int c = 0; c < CPL; ++c) ch[rg][c] = S[rg][0].get(c) * kh[rg];
+#pragma unroll
+    for (int i = 1; i < kRowsPerLane; ++i) {
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) ch[rg][c] = fmaf(S[rg][i].get(c), kh[rg + kRowGroups * i], ch[rg][c]);
+    }
+  }
+  float delta[CPL];
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    const float kv = scan_column_sum(ch[0][c], ch[1][c], ch[2][c], ch[3][c]);
+    delta[c] = (v[c] - alpha * kv) * beta;
+  }
+#pragma unroll
+  for (int rg = 0; rg < kRowGroups; ++rg) {
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) ch[rg][c] = 0.f;
+#pragma unroll
+    for (int i = 0; i < kRowsPerLane; ++i) {
+      const int r = rg + kRowGroups * i;
+#pragma unroll
+      for (int c = 0; c < CPL; c += 2) {
+        const float n0 = fmaf(alpha, S[rg][i].get(c), kh[r] * delta[c]);
+        const float n1 = fmaf(alpha, S[rg][i].get(c + 1), kh[r] * delta[c + 1]);
+        S[rg][i].set2(c, n0, n1);
+        ch[rg][c] = fmaf(n0, qh[r], ch[rg][c]);
+        ch[rg][c + 1] = fmaf(n1, qh[r], ch[rg][c + 1]);
+      }
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < CPL; ++c)
+    y[c] = scan_column_sum(ch[0][c], ch[1][c], ch[2][c], ch[3][c]) * kYScale;
 }
 
 // Computes one token's gates ONCE per tile and leaves them in lds.gate for
