@@ -32,6 +32,8 @@ BASELINE shapes, each captured in a hipGraph and timed with events:
   quantize_act      [64, 4096] bf16 (both launches)
   readout_quant_*   gated RMSNorm readout + out_proj input FP8 quant (both
                     launches), 64 decode tokens and config 2's 4073 tokens
+  fp8_gemm_*        config 3's FP8 projection GEMMs at B=64 through hipBLASLt
+                    (bytes: fp8 weight + x + bf16 out), torch._scaled_mm beside
   mixer_step        config 3: 24 GDN layers of quant -> conv -> gated decode ->
                     readout + quant at B=64, one fp16 pool and conv pool per
                     layer
@@ -303,6 +305,24 @@ def measure_paths(torch, kern):
                       "gbs": round(rbytes / t / 1e9, 1),
                       "hbm_frac": round(rbytes / t / 1e9 / HBM_PEAK_GBS, 4)}
         del ry, rz
+
+    # FP8 projection GEMMs of config 3's layer at B=64 (hipBLASLt): in_proj
+    # qkv + z (N = 8192 + 4096) and out_proj (N = 4096), K = 4096; HBM-bound
+    # on the fp8 weight bytes
+    xg = torch.randn(64, 4096, generator=g, device=dev).to(torch.bfloat16)
+    xgq, sxg = kern.quantize_act(xg)
+    for label, N in (("fp8_gemm_in_proj_b64", 12288), ("fp8_gemm_out_proj_b64", 4096)):
+        wq, sw = kern.quantize_act(torch.randn(N, 4096, generator=g, device=dev) * 0.02)
+        t = graph_time(torch, lambda: kern.fp8_matmul(xgq, sxg, wq, sw), reps=5, inner=20)
+        t_ref = graph_time(torch, lambda: torch._scaled_mm(xgq, wq.t(), scale_a=sxg, scale_b=sw,
+                                                           out_dtype=torch.bfloat16),
+                           reps=5, inner=20)
+        gbytes = N * 4096 + 64 * 4096 + 64 * N * 2
+        out[label] = {"shape": f"M=64 N={N} K=4096", "us": round(t * 1e6, 2),
+                      "gbs": round(gbytes / t / 1e9, 1),
+                      "hbm_frac": round(gbytes / t / 1e9 / HBM_PEAK_GBS, 4),
+                      "torch_scaled_mm_us": round(t_ref * 1e6, 2)}
+        del wq
 
     # config 3: 24-layer mixer decode step at B=64
     L, Bm, S = 24, 64, 72

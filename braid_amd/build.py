@@ -30,7 +30,10 @@ LIB = PKG / "libbraid_gdn.so"
 OBJ_DIR = PKG / "_build"
 
 SOURCES = ["capi_common.cpp", "gdn_scan.hip", "conv1d_decode.hip", "quant_act.hip",
-           "gated_norm.hip"]
+           "gated_norm.hip", "fp8_gemm.cpp"]
+# hipBLASLt for the FP8 GEMM. Its SONAME (libhipblaslt.so.1) matches the copy
+# torch loads, so in a torch process the library binds to that one.
+LIBS = ["-L/opt/rocm/lib", "-lhipblaslt"]
 
 ARCH = os.environ.get("BRAID_OFFLOAD_ARCH", "gfx950")
 
@@ -72,7 +75,7 @@ def build(verbose: bool = False, defines: tuple = (), lib: Path = LIB) -> Path:
     with ThreadPoolExecutor(max_workers=min(4, len(SOURCES))) as ex:
         objs = list(ex.map(lambda s: _compile(s, defines, obj_dir), SOURCES))
     tmp = lib.with_suffix(".so.tmp")
-    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs),
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), *LIBS,
            "-o", str(tmp)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:

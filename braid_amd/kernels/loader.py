@@ -61,6 +61,9 @@ SIGNATURES = {
     "braid_quantize_act_workspace": ([_i64], _i32),
     "braid_quantize_act": ([_vp, _i32, _i64, _vp, _vp, _vp, _vp], _i32),
     "braid_gated_rmsnorm_workspace": ([_i64], _i32),
+    "braid_fp8_gemm_workspace": ([], ctypes.c_size_t),
+    "braid_fp8_gemm": ([_vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _vp, ctypes.c_size_t,
+                        _vp], _i32),
     "braid_gated_rmsnorm_quant": ([_vp, _i32, _vp, _i32, _vp, ctypes.c_float, _i64, _i32, _vp,
                                    _vp, _vp, _vp, _vp], _i32),
 }
@@ -139,6 +142,7 @@ class GDNKernels:
     def __init__(self, lib: ctypes.CDLL):
         self._lib = lib
         self.abi_version = lib.braid_abi_version()
+        self._workspaces: dict = {}
 
     # -- plumbing -------------------------------------------------------------
 
@@ -365,6 +369,41 @@ class GDNKernels:
                    _ptr(z), _QUANT_DTYPES[z.dtype], _ptr(gamma), float(eps), units, HD,
                    _ptr(core), _ptr(q), _ptr(scale), _ptr(partial))
         return (core, q, scale) if quantize else core
+
+    # -- FP8 GEMM (hipBLASLt) ------------------------------------------------------
+
+    def _gemm_workspace(self, device: torch.device) -> torch.Tensor:
+        """One workspace per device, allocated on first use (outside any graph
+        capture, since the first call of a shape also selects its algorithm)."""
+        key = torch.device(device).index or 0
+        ws = self._workspaces.get(key)
+        if ws is None:
+            ws = torch.empty(self._lib.braid_fp8_gemm_workspace(), dtype=torch.uint8,
+                             device=device)
+            self._workspaces[key] = ws
+        return ws
+
+    def fp8_matmul(self, xq: torch.Tensor, sx: torch.Tensor, w: torch.Tensor,
+                   sw: torch.Tensor, out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+        """``torch._scaled_mm(xq, w.t(), scale_a=sx, scale_b=sw, out_dtype)``
+        (braid/model/quant.py:232-241): xq [M, K] and w [N, K] float8_e4m3fn,
+        sx / sw one-element fp32 dequant scales; returns [M, N]."""
+        fp8 = torch.float8_e4m3fn
+        _check(xq.is_cuda and w.is_cuda and sx.is_cuda and sw.is_cuda, "operands must be cuda")
+        _check(xq.dtype == fp8 and w.dtype == fp8, "xq and w must be float8_e4m3fn")
+        _check(xq.dim() == 2 and w.dim() == 2 and xq.size(1) == w.size(1),
+               "xq must be [M, K] and w [N, K]")
+        _check(xq.is_contiguous() and w.is_contiguous(), "xq and w must be contiguous")
+        _check(sx.dtype == torch.float32 and sw.dtype == torch.float32
+               and sx.numel() == 1 and sw.numel() == 1, "scales must be one fp32 element each")
+        _check(out_dtype in _QUANT_DTYPES, "out dtype must be bf16, fp16 or fp32")
+        M, K = xq.shape
+        N = w.size(0)
+        out = torch.empty(M, N, dtype=out_dtype, device=xq.device)
+        ws = self._gemm_workspace(xq.device)
+        self._call("braid_fp8_gemm", xq.device, _ptr(xq), _ptr(sx), _ptr(w), _ptr(sw), _ptr(out),
+                   _QUANT_DTYPES[out_dtype], M, N, K, _ptr(ws), ws.numel())
+        return out
 
 
 @lru_cache(maxsize=1)

@@ -22,6 +22,7 @@
 #ifndef BRAID_GDN_H
 #define BRAID_GDN_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -204,6 +205,32 @@ int braid_gated_rmsnorm_quant(const void* y, int y_dtype, const void* z,
                               int act_dtype, const float* gamma, float eps,
                               int64_t units, int HD, void* core, uint8_t* q,
                               float* scale, float* partial, void* stream);
+
+/*
+ * Workspace bytes braid_fp8_gemm plans for (the algorithm it selects needs at
+ * most this much).
+ */
+size_t braid_fp8_gemm_workspace(void);
+
+/*
+ * FP8 e4m3fn W8A8 GEMM with per-tensor dequant scales, through hipBLASLt.
+ * Replaces fp8_matmul's torch._scaled_mm(xq, w.t(), scale_a=sx, scale_b=sw)
+ * (braid/model/quant.py:232-241).
+ *
+ *   x        [M, K] e4m3fn codes, row-major (the quantized activation)
+ *   x_scale  [1] fp32 device: x's dequant scale
+ *   w        [N, K] e4m3fn codes, row-major (the weight, as FP8Weight.data)
+ *   w_scale  [1] fp32 device
+ *   out      [M, N] of out_dtype (BRAID_BF16, F16 or F32), row-major:
+ *            out = (x * x_scale) @ (w * w_scale)^T, fp32 accumulation
+ *   workspace  device scratch of workspace_bytes (>= braid_fp8_gemm_workspace())
+ * N and K must be multiples of 16. The first call for a shape selects the
+ * algorithm on the host; later calls only enqueue, and may be captured.
+ */
+int braid_fp8_gemm(const uint8_t* x, const float* x_scale, const uint8_t* w,
+                   const float* w_scale, void* out, int out_dtype, int64_t M,
+                   int64_t N, int64_t K, void* workspace,
+                   size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }
