@@ -34,9 +34,8 @@ BASELINE shapes, each captured in a hipGraph and timed with events:
                     launches), 64 decode tokens and config 2's 4073 tokens
   fp8_gemm_*        config 3's FP8 projection GEMMs at B=64 through hipBLASLt
                     (bytes: fp8 weight + x + bf16 out), torch._scaled_mm beside
-  mixer_step        config 3: 24 GDN layers of quant -> conv -> gated decode ->
-                    readout + quant at B=64, one fp16 pool and conv pool per
-                    layer
+  mixer_step        config 3: 24 GDN layers of quant -> conv -> gated decode at
+                    B=64, one fp16 pool and conv pool per layer
   mixed_tick        config 4: 4 x 256-token prefill + 96 decode rows on one
                     192-slot fp16 pool; eager and graph-replayed per bucket
 
@@ -337,8 +336,7 @@ def measure_paths(torch, kern):
             xin=torch.randn(Bm, C, generator=g, device=dev).to(torch.bfloat16),
             a=torch.randn(Bm, H, generator=g, device=dev).to(torch.bfloat16),
             b=torch.randn(Bm, H, generator=g, device=dev).to(torch.bfloat16),
-            cout=torch.empty(Bm, C, device=dev), y=torch.empty(Bm, H, D, device=dev),
-            z=torch.randn(Bm, H * D, generator=g, device=dev).to(torch.bfloat16)))
+            cout=torch.empty(Bm, C, device=dev), y=torch.empty(Bm, H, D, device=dev)))
 
     def mixer_step():
         for ly in layers:
@@ -348,11 +346,9 @@ def measure_paths(torch, kern):
             kern.gdn_decode_raw(ly["pool"], slots64, q.unflatten(-1, (G, D)),
                                 k.unflatten(-1, (G, D)), v.unflatten(-1, (H, D)), ly["a"],
                                 ly["b"], A, dtb, ly["y"])
-            kern.gated_rmsnorm(ly["y"], ly["z"], gamma, 1e-6)
 
     t = graph_time(torch, mixer_step, reps=5)
-    step_bytes = L * (QUANT_BYTES_64x4096 + CONV_BYTES_B64 + Bm * ROW_BYTES
-                      + Bm * H * D * READOUT_BYTES_PER_ELEM)
+    step_bytes = L * (QUANT_BYTES_64x4096 + CONV_BYTES_B64 + Bm * ROW_BYTES)
     out["mixer_step"] = {"layers": L, "batch": Bm, "us": round(t * 1e6, 1),
                          "gbs": round(step_bytes / t / 1e9, 1),
                          "hbm_frac": round(step_bytes / t / 1e9 / HBM_PEAK_GBS, 4),
