@@ -10,19 +10,11 @@
 // registers (in the pool's storage type) and stores it once. Reference behaviour: braid/kernels/csrc/gdn_decode.cu:156-272 (decode)
 // and :467-551 (prefill); entry-point contracts :313-441 and :553-699.
 #include "capi_common.h"
+#include "conv_common.h"
 #include "gdn_tile.h"
 
 namespace braid {
 namespace {
-
-template <class Tag>
-struct Storage;
-template <>
-struct Storage<F32> { using T = float; };
-template <>
-struct Storage<F16> { using T = uint16_t; };
-template <>
-struct Storage<BF16> { using T = uint16_t; };
 
 // One decode token for the tile (blockIdx.x = b * H + h).
 template <class Tag, class Gates>
@@ -62,6 +54,72 @@ gdn_decode_kernel(typename Storage<Tag>::T* __restrict__ pool, const int* __rest
 #pragma unroll
   for (int i = 0; i < kRowsPerLane; ++i) S[i].store_nt(tile + (size_t)L.row(i) * kHD);
   // Each column's totals sit in all lanes of its chunk; one lane per chunk writes them.
+  if (L.stores_y()) storeN<CPL>(y + ((size_t)b * H + h) * kHD + L.col0, yy);
+}
+
+// The conv1d decode step fused into the GDN decode step (one launch for the
+// mixer's conv and recurrence): one workgroup per (batch row b, key group g)
+// owns the HPG value heads of the group, HPG tiles of four waves each. Its
+// threads first run the conv step (conv_step, the conv kernels' arithmetic)
+// for the group's q and k channels and the heads' v channels, updating those
+// channels' windows in the conv pool and leaving the outputs in LDS; then each
+// tile runs the decode token on them exactly as gdn_decode_kernel does on q/k/v
+// read from memory. So the outputs, the state and the windows equal
+// conv1d_decode followed by gdn_decode, bit for bit. A group's q/k windows are
+// advanced once because one workgroup owns all heads that read them. The conv
+// outputs never go to memory: nothing but the recurrence reads them.
+template <int HPG>
+struct ConvDecodeLds {
+  TileLds tile[HPG];
+  float qkv[2 + HPG][kHD];  // conv outputs: q, k, then each head's v
+};
+
+template <class Tag, class XT, class Gates, int HPG>
+__global__ void __launch_bounds__(tile_threads(kDecodeCols) * HPG)
+gdn_conv_decode_kernel(typename Storage<Tag>::T* __restrict__ pool,
+                       float* __restrict__ conv_pool, const int* __restrict__ slot_idx,
+                       const XT* __restrict__ x, const float* __restrict__ conv_w,
+                       const float* __restrict__ conv_b, Gates gates, float* __restrict__ y,
+                       int H, int G, int C) {
+  constexpr int CPL = kDecodeCols, kK = 4;
+  constexpr int kTileThreads = tile_threads(CPL);
+  using ST = typename Storage<Tag>::T;
+  const int b = blockIdx.x / G;
+  const int g = blockIdx.x - b * G;
+  const int t = threadIdx.x / kTileThreads;
+  const int h = g * HPG + t;
+  const LaneMap<CPL> L(threadIdx.x % kTileThreads);
+
+  __shared__ ConvDecodeLds<HPG> lds;
+  const int slot = slot_idx[b];
+  ST* tile = pool + ((size_t)slot * H + h) * (kSS * kHD) + L.col0;
+  Row<Tag, CPL> S[kRowsPerLane];
+#pragma unroll
+  for (int i = 0; i < kRowsPerLane; ++i) S[i].load_nt(tile + (size_t)L.row(i) * kHD);
+
+  // Conv for the group's channels: segment 0 = q (channels g*SS..), 1 = k
+  // (G*SS + g*SS..), 2 + j = v of head g*HPG + j (2*G*SS + head*HD..).
+  for (int e = threadIdx.x; e < (2 + HPG) * kHD; e += kTileThreads * HPG) {
+    const int seg = e / kHD, off = e - seg * kHD;
+    const int c = seg < 2 ? seg * G * kSS + g * kSS + off
+                          : 2 * G * kSS + (g * HPG + seg - 2) * kHD + off;
+    float* st = conv_pool + ((size_t)slot * C + c) * kK;
+    float w[kK], wt[kK];
+    load_window<kK>(st, conv_w + (size_t)c * kK, w, wt);
+    lds.qkv[seg][off] = conv_step<kK>(w, conv_widen(x[(size_t)b * C + c]), wt, conv_b, c);
+    store_window<kK>(st, w);
+  }
+  __syncthreads();
+
+  float vv[CPL];
+  loadN<CPL>(&lds.qkv[2 + t][L.col0], vv);
+  QK qk;
+  normalize_qk(L, lds.qkv[0], lds.qkv[1], qk);
+  publish_gates(L, gates, gates.load(b, h, 0, H, 1), h, lds.tile[t]);
+  float yy[CPL];
+  gdn_token<Tag, CPL>(L, S, qk, vv, lds.tile[t], lds.tile[t].gate, yy);
+#pragma unroll
+  for (int i = 0; i < kRowsPerLane; ++i) S[i].store_nt(tile + (size_t)L.row(i) * kHD);
   if (L.stores_y()) storeN<CPL>(y + ((size_t)b * H + h) * kHD + L.col0, yy);
 }
 
@@ -409,4 +467,94 @@ extern "C" int braid_gdn_prefill_raw(void* pool, int pool_dtype, int64_t n_slots
   RawGates<BF16> gates{static_cast<const uint16_t*>(a_raw), static_cast<const uint16_t*>(b_raw),
                        A, dt_bias, seq_lens};
   return launch_prefill(pool, pool_dtype, slot_idx, B, T, H, G, q, k, v, gates, y, stream);
+}
+
+namespace braid {
+namespace {
+
+template <class Tag, class XT, class Gates, int HPG>
+void launch_conv_decode_as(void* pool, float* conv_pool, const int32_t* slot_idx, int B, int H,
+                           int G, int C, const void* x, const float* w, const float* bias,
+                           Gates gates, float* y, hipStream_t stream) {
+  const dim3 grid((unsigned)B * (unsigned)G), block(tile_threads(kDecodeCols) * HPG);
+  gdn_conv_decode_kernel<Tag, XT, Gates, HPG><<<grid, block, 0, stream>>>(
+      static_cast<typename Storage<Tag>::T*>(pool), conv_pool, slot_idx,
+      static_cast<const XT*>(x), w, bias, gates, y, H, G, C);
+}
+
+template <class Tag, class XT, class Gates>
+void launch_conv_decode_hpg(int hpg, void* pool, float* conv_pool, const int32_t* slot_idx,
+                            int B, int H, int G, int C, const void* x, const float* w,
+                            const float* bias, Gates gates, float* y, hipStream_t stream) {
+  if (hpg == 1)
+    launch_conv_decode_as<Tag, XT, Gates, 1>(pool, conv_pool, slot_idx, B, H, G, C, x, w, bias,
+                                             gates, y, stream);
+  else
+    launch_conv_decode_as<Tag, XT, Gates, 2>(pool, conv_pool, slot_idx, B, H, G, C, x, w, bias,
+                                             gates, y, stream);
+}
+
+template <class XT, class Gates>
+void launch_conv_decode(int pool_dtype, int hpg, void* pool, float* conv_pool,
+                        const int32_t* slot_idx, int B, int H, int G, int C, const void* x,
+                        const float* w, const float* bias, Gates gates, float* y,
+                        hipStream_t stream) {
+  switch (pool_dtype) {
+    case BRAID_F32:
+      launch_conv_decode_hpg<F32, XT, Gates>(hpg, pool, conv_pool, slot_idx, B, H, G, C, x, w,
+                                             bias, gates, y, stream);
+      break;
+    case BRAID_F16:
+      launch_conv_decode_hpg<F16, XT, Gates>(hpg, pool, conv_pool, slot_idx, B, H, G, C, x, w,
+                                             bias, gates, y, stream);
+      break;
+    default:
+      launch_conv_decode_hpg<BF16, XT, Gates>(hpg, pool, conv_pool, slot_idx, B, H, G, C, x, w,
+                                              bias, gates, y, stream);
+      break;
+  }
+}
+
+}  // namespace
+}  // namespace braid
+
+extern "C" int braid_gdn_conv_decode_raw(void* pool, int pool_dtype, int64_t n_slots, int H,
+                                         int G, int SS, int HD, float* conv_pool, int K,
+                                         const int32_t* slot_idx, int B, const void* x,
+                                         int x_dtype, const float* conv_weight,
+                                         const float* conv_bias, const void* a_raw,
+                                         const void* b_raw, int act_dtype, const float* A,
+                                         const float* dt_bias, float* y, void* stream_) {
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  BRAID_TRY(check_common(pool, pool_dtype, n_slots, H, G, SS, HD, slot_idx, B));
+  BRAID_TRY(check_act(a_raw, b_raw, act_dtype, A, dt_bias));
+  const int hpg = H / G;
+  if (hpg != 1 && hpg != 2)
+    return fail(BRAID_EINVAL, "the fused conv decode takes 1 or 2 value heads per key group");
+  if (K != 4) return fail(BRAID_EINVAL, "the fused conv decode takes conv_kernel == 4");
+  if (x_dtype != BRAID_F32 && x_dtype != BRAID_BF16)
+    return fail(BRAID_EINVAL, "x must be fp32 or bf16 (the activation dtypes braid runs)");
+  if (B == 0) return ok();
+  if (conv_pool == nullptr || x == nullptr || conv_weight == nullptr)
+    return fail(BRAID_EINVAL, "conv_pool, x and conv_weight must be non-null");
+  if (!aligned16(conv_pool) || !aligned16(conv_weight))
+    return fail(BRAID_EINVAL, "conv_pool and conv_weight must be 16-byte aligned");
+  BRAID_TRY(check_dense(y, "y"));
+  BRAID_TRY(validate_slots(slot_idx, B, n_slots, true, stream));
+  const int C = 2 * G * SS + H * HD;
+  auto go = [&](auto gates) {
+    if (x_dtype == BRAID_F32)
+      launch_conv_decode<float>(pool_dtype, hpg, pool, conv_pool, slot_idx, B, H, G, C, x,
+                                conv_weight, conv_bias, gates, y, stream);
+    else
+      launch_conv_decode<uint16_t>(pool_dtype, hpg, pool, conv_pool, slot_idx, B, H, G, C, x,
+                                   conv_weight, conv_bias, gates, y, stream);
+    const int st = hip_status(hipGetLastError(), "launching gdn_conv_decode_kernel");
+    return st != BRAID_OK ? st : ok();
+  };
+  if (act_dtype == BRAID_F32)
+    return go(RawGates<F32>{static_cast<const float*>(a_raw), static_cast<const float*>(b_raw),
+                            A, dt_bias, nullptr});
+  return go(RawGates<BF16>{static_cast<const uint16_t*>(a_raw),
+                           static_cast<const uint16_t*>(b_raw), A, dt_bias, nullptr});
 }

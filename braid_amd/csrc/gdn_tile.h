@@ -110,6 +110,16 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, bf16x2));
 }
 
+// Element type of a pool of each storage tag.
+template <class Tag>
+struct Storage;
+template <>
+struct Storage<F32> { using T = float; };
+template <>
+struct Storage<F16> { using T = uint16_t; };
+template <>
+struct Storage<BF16> { using T = uint16_t; };
+
 template <class Tag, int N>
 struct Row;
 

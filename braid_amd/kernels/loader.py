@@ -54,6 +54,9 @@ SIGNATURES = {
     "braid_gdn_prefill_raw": ([_vp, _i32, _i64, _i32, _i32, _i32, _i32, _vp, _i32, _i32,
                                _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp,
                                _vp], _i32),
+    "braid_gdn_conv_decode_raw": ([_vp, _i32, _i64, _i32, _i32, _i32, _i32, _vp, _i32, _vp,
+                                   _i32, _vp, _i32, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp,
+                                   _vp], _i32),
     "braid_conv1d_decode": ([_vp, _i64, _i32, _i32, _vp, _i32, _vp, _i32, _vp, _vp,
                              _vp, _vp], _i32),
     "braid_conv1d_prefill": ([_vp, _i64, _i32, _i32, _vp, _i32, _i32, _vp, _i32, _vp, _vp,
@@ -189,6 +192,45 @@ class GDNKernels:
         self._call("braid_gdn_decode_raw", pool.device, _ptr(pool), pdt, pool.size(0), H, G,
                    SS, HD, _ptr(slot_idx), B, _ptr(q), q_row, _ptr(k), k_row, _ptr(v), v_row,
                    _ptr(a_raw), _ptr(b_raw), adt, _ptr(A), _ptr(dt_bias), _ptr(y))
+
+    def gdn_conv_decode_raw(self, pool, conv_pool, slot_idx, x, weight, bias, a_raw, b_raw,
+                            A, dt_bias, y, n_groups: int) -> None:
+        """conv1d_decode then gdn_decode_raw on the conv output's q/k/v views,
+        fused in one launch with the same bits (gdn.py:131-160). x [B, C] is
+        the pre-conv projection (fp32 or bf16), C = 2 * n_groups * 128 + H * 128;
+        the conv output is not materialised."""
+        pdt = _check_pool(pool, slot_idx)
+        _check(conv_pool.is_cuda and conv_pool.dtype == torch.float32
+               and conv_pool.is_contiguous() and conv_pool.dim() == 3,
+               "conv_pool must be contiguous cuda fp32 [S_max, C, K]")
+        _check(y.is_cuda and y.dtype == torch.float32 and y.is_contiguous(),
+               "y must be contiguous cuda fp32")
+        adt = _check_raw(a_raw, b_raw, A, dt_bias)
+        n_slots, H, SS, HD = pool.shape
+        G = int(n_groups)
+        _check(G > 0 and H % G == 0, "n_heads must be divisible by n_groups")
+        C, K = conv_pool.size(1), conv_pool.size(2)
+        _check(C == 2 * G * SS + H * HD, "conv_pool channels must be 2*G*SS + H*HD")
+        _check(conv_pool.size(0) == n_slots, "conv_pool and pool must hold the same slots")
+        _check(x.dim() == 2 and x.size(1) == C, "x must be [B, C]")
+        B = x.size(0)
+        _check(x.dtype in _ACT_DTYPES, "x must be fp32 or bf16 (the activation dtypes braid runs)")
+        _check(x.is_cuda and x.is_contiguous(), "x must be contiguous")
+        _check(tuple(weight.shape) == (C, K), "weight must be [C, K]")
+        _check_dense_f32((weight,), "weight must be contiguous cuda fp32")
+        bias_p = None
+        if bias is not None and bias.numel() > 0:
+            _check_dense_f32((bias,), "bias must be contiguous cuda fp32")
+            _check(bias.numel() == C, "bias must be [C]")
+            bias_p = _ptr(bias)
+        _check(slot_idx.numel() == B, "slot_idx must have one entry per batch row")
+        _check(tuple(y.shape) == (B, H, HD), "y shape must be [B, H, HD]")
+        _check(a_raw.numel() == B * H and b_raw.shape == a_raw.shape, "a_raw/b_raw must be [B, H]")
+        _check(A.numel() == H and dt_bias.numel() == H, "A and dt_bias must be [H]")
+        self._call("braid_gdn_conv_decode_raw", pool.device, _ptr(pool), pdt, n_slots, H, G, SS,
+                   HD, _ptr(conv_pool), K, _ptr(slot_idx), B, _ptr(x), _ACT_DTYPES[x.dtype],
+                   _ptr(weight), bias_p, _ptr(a_raw), _ptr(b_raw), adt, _ptr(A), _ptr(dt_bias),
+                   _ptr(y))
 
     @staticmethod
     def _check_decode_shapes(pool, slot_idx, q, k, v, y, B, G, SS, H, HD) -> None:

@@ -14,6 +14,9 @@ build has and the reference had not:
 * prefill's causal conv runs ``conv1d_prefill`` (one launch, window saved in
   place) instead of ``F.conv1d`` over ``[window | x]`` plus a gather
   (gdn.py:193-222); outputs and windows equal ``conv1d_decode`` token by token;
+* decode runs the conv and the recurrence as one launch
+  (``gdn_conv_decode_raw``) where the shape allows, instead of
+  ``conv1d_decode`` then ``gdn_decode_raw`` (gdn.py:131-160), same bits;
 * the readout runs ``gated_rmsnorm`` (norm, gate and, for an FP8 out_proj,
   the activation quantization in two launches) instead of the torch norm and
   ``quantize_act``.
@@ -52,6 +55,10 @@ class GDNMixerLayer:
         self.dt_bias = weights["dt_bias"].float().contiguous()
         self.norm = weights["norm"].float().contiguous()
         self._mod = load_gdn()
+        # The fused conv + recurrence launch covers conv kernel 4 with one or
+        # two value heads per key group (every Qwen3.5 GDN layer); other shapes
+        # run the two kernels. Either way the bits are the same.
+        self.fused_decode = (g.conv_kernel == 4 and g.n_heads // g.n_groups in (1, 2))
 
     def _split(self, conv_out: torch.Tensor):
         """[..., C] -> q, k [..., G, SS] and v [..., H, HD]; Q | K | V, Q first
@@ -69,15 +76,24 @@ class GDNMixerLayer:
     def decode(self, qkv_proj: torch.Tensor, z: torch.Tensor, a_raw: torch.Tensor,
                b_raw: torch.Tensor, cache: RecurrentCache, slots_i32: torch.Tensor):
         """One token for every row: qkv_proj [B, 1, C], z [B, 1, H*HD],
-        a_raw / b_raw [B, 1, H] (gdn.py:107-167 with raw gates, then _readout)."""
+        a_raw / b_raw [B, 1, H] (gdn.py:107-167 with raw gates, then _readout).
+        The conv and the recurrence run as one fused launch when the shape
+        allows it (conv kernel 4, one or two value heads per key group), with
+        the same bits as the two kernels back to back."""
         g = self.g
         B = qkv_proj.shape[0]
         qkv = qkv_proj[:, 0]
+        y = torch.empty(B, 1, g.n_heads, g.head_dim, device=qkv.device, dtype=torch.float32)
+        if self.fused_decode:
+            self._mod.gdn_conv_decode_raw(cache.state, cache.conv, slots_i32, qkv.contiguous(),
+                                          self.conv1d_f32, self.conv_bias_f32,
+                                          a_raw[:, 0].contiguous(), b_raw[:, 0].contiguous(),
+                                          self.A, self.dt_bias, y[:, 0], g.n_groups)
+            return self._readout(z, y)
         conv_out = torch.empty(qkv.shape, device=qkv.device, dtype=torch.float32)
         self._mod.conv1d_decode(cache.conv, slots_i32, qkv.contiguous(), self.conv1d_f32,
                                 self.conv_bias_f32, conv_out)
         q, k, v = self._split(conv_out)
-        y = torch.empty(B, 1, g.n_heads, g.head_dim, device=qkv.device, dtype=torch.float32)
         self._mod.gdn_decode_raw(cache.state, slots_i32, q, k, v, a_raw[:, 0].contiguous(),
                                  b_raw[:, 0].contiguous(), self.A, self.dt_bias, y[:, 0])
         return self._readout(z, y)

@@ -88,6 +88,29 @@ int braid_gdn_decode_raw(void* pool, int pool_dtype, int64_t n_slots, int H,
                          void* stream);
 
 /*
+ * The conv1d decode step fused into the GDN decode step with in-kernel gates:
+ * braid_conv1d_decode followed by braid_gdn_decode_raw on the conv output's
+ * q/k/v column views, in one launch and bit for bit the same outputs, state
+ * and windows. Replaces the pair the reference's decode runs back to back
+ * (braid/model/gdn.py:131-160: conv1d_decode, then gdn_decode_raw on
+ * split/unflatten views of its output); the conv output is not written.
+ *
+ *   conv_pool [n_slots, C, K] fp32 with C = 2*G*SS + H*HD ([Q | K | V]);
+ *             K must be 4; updated in place at the slot rows
+ *   x         [B, C] of x_dtype (BRAID_F32 or BRAID_BF16), dense
+ *   conv_weight [C, K] fp32; conv_bias [C] fp32 or NULL
+ *   H / G must be 1 or 2. Other arguments as braid_gdn_decode_raw; slots must
+ *   be distinct.
+ */
+int braid_gdn_conv_decode_raw(void* pool, int pool_dtype, int64_t n_slots, int H,
+                              int G, int SS, int HD, float* conv_pool, int K,
+                              const int32_t* slot_idx, int B, const void* x,
+                              int x_dtype, const float* conv_weight,
+                              const float* conv_bias, const void* a_raw,
+                              const void* b_raw, int act_dtype, const float* A,
+                              const float* dt_bias, float* y, void* stream);
+
+/*
  * Chunk prefill scan: T tokens per launch, state held on chip between them.
  * Replaces gdn_prefill (gdn_decode.cu:553-603).
  *
