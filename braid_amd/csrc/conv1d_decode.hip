@@ -70,12 +70,13 @@ __device__ __forceinline__ void load_x(const uint16_t* p, float (&o)[NC]) {
     o[0] = conv_widen(*p);
   }
 }
+// Prefill outputs are written once and read by a later launch: nontemporal.
 template <int NC>
 __device__ __forceinline__ void store_out(float* p, const float (&o)[NC]) {
   if constexpr (NC == 4) {
-    *reinterpret_cast<f32x4*>(p) = (f32x4){o[0], o[1], o[2], o[3]};
+    __builtin_nontemporal_store((f32x4){o[0], o[1], o[2], o[3]}, reinterpret_cast<f32x4*>(p));
   } else {
-    *p = o[0];
+    __builtin_nontemporal_store(o[0], p);
   }
 }
 

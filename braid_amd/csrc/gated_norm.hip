@@ -84,16 +84,17 @@ __device__ __forceinline__ void load4(Tag tag, const uint16_t* p, long i, float 
     o[e] = widen(tag, (uint16_t)((r[e >> 1] >> (16 * (e & 1))) & 0xffffu));
 }
 
-// Rounds o[0..3] to the act dtype in place and stores them at p + i.
+// Rounds o[0..3] to the act dtype in place and stores them at p + i
+// (nontemporal: core is read back once, by the quantize pass or out_proj).
 __device__ __forceinline__ void round_store4(XF32, float* p, long i, float (&o)[4]) {
-  *reinterpret_cast<f32x4*>(p + i) = (f32x4){o[0], o[1], o[2], o[3]};
+  __builtin_nontemporal_store((f32x4){o[0], o[1], o[2], o[3]}, reinterpret_cast<f32x4*>(p + i));
 }
 template <class Tag>
 __device__ __forceinline__ void round_store4(Tag, uint16_t* p, long i, float (&o)[4]) {
   uint32_t r0, r1;
   Narrow<Tag>::pair(o[0], o[1], r0);
   Narrow<Tag>::pair(o[2], o[3], r1);
-  *reinterpret_cast<u32x2*>(p + i) = (u32x2){r0, r1};
+  __builtin_nontemporal_store((u32x2){r0, r1}, reinterpret_cast<u32x2*>(p + i));
 }
 template <class Tag>
 __device__ __forceinline__ void round4(Tag, float (&o)[4]) {
@@ -102,8 +103,38 @@ __device__ __forceinline__ void round4(Tag, float (&o)[4]) {
   Narrow<Tag>::pair(o[2], o[3], unused);
 }
 
+// One unit's computation from its loaded y (c, widened) and z values: writes
+// core and folds |core| into the running max m.
+template <class ATag>
+__device__ __forceinline__ void gated_unit(float (&c)[4], const float (&zf)[4], const f32x4& gm,
+                                           float eps, bool live, typename ATag::T* core, long i,
+                                           float& m) {
+  round4(ATag{}, c);
+  float ss = (c[0] * c[0] + c[1] * c[1]) + (c[2] * c[2] + c[3] * c[3]);
+#pragma unroll
+  for (int s = 1; s < kLanesPerUnit; s <<= 1) ss += __shfl_xor(ss, s, 64);
+  const float r = rsqrtf(ss * (1.0f / kUnit) + eps);  // mean: exact power-of-two scale
+  float o[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) o[e] = c[e] * r;
+  round4(ATag{}, o);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float h = gm[e] * o[e];
+    const float s = zf[e] / (1.0f + expf(-zf[e]));
+    o[e] = h * s;
+  }
+  if (live) {
+    round_store4(ATag{}, core, i, o);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) m = nan_max(m, fabsf(o[e]));
+  }
+}
+
 // YTag: dtype of the scan output y (fp32, or already the act dtype). ATag: the
-// act dtype of z and core.
+// act dtype of z and core. Each wave iteration takes two pairs of units (the
+// pair at u0 and the pair a grid step further), loading all four units'
+// inputs before computing any, so more loads are in flight.
 template <class YTag, class ATag>
 __global__ void __launch_bounds__(kThreads)
 gated_norm_amax(const typename YTag::T* __restrict__ y, const typename ATag::T* __restrict__ z,
@@ -116,35 +147,22 @@ gated_norm_amax(const typename YTag::T* __restrict__ y, const typename ATag::T* 
   const long step = (long)gridDim.x * kUnitsPerBlock;
   // Both halves of a wave run every iteration (the butterfly needs all 64
   // lanes); a half past the end works on zeros and stores nothing.
-  for (long u0 = ((long)blockIdx.x * (kThreads / 64) + wave) * 2; u0 < units; u0 += step) {
-    const long u = u0 + half;
-    const bool live = u < units;
-    const long i = u * kUnit + 4 * sub;
-    float c[4] = {0.f, 0.f, 0.f, 0.f}, zf[4] = {0.f, 0.f, 0.f, 0.f};
-    if (live) {
-      load4(YTag{}, y, i, c);
-      load4(ATag{}, z, i, zf);
+  for (long u0 = ((long)blockIdx.x * (kThreads / 64) + wave) * 2; u0 < units; u0 += 2 * step) {
+    const long ua = u0 + half, ub = u0 + step + half;
+    const bool la = ua < units, lb = ub < units;
+    const long ia = ua * kUnit + 4 * sub, ib = ub * kUnit + 4 * sub;
+    float ca[4] = {0.f, 0.f, 0.f, 0.f}, za[4] = {0.f, 0.f, 0.f, 0.f};
+    float cb[4] = {0.f, 0.f, 0.f, 0.f}, zb[4] = {0.f, 0.f, 0.f, 0.f};
+    if (la) {
+      load4(YTag{}, y, ia, ca);
+      load4(ATag{}, z, ia, za);
     }
-    round4(ATag{}, c);
-    float ss = (c[0] * c[0] + c[1] * c[1]) + (c[2] * c[2] + c[3] * c[3]);
-#pragma unroll
-    for (int s = 1; s < kLanesPerUnit; s <<= 1) ss += __shfl_xor(ss, s, 64);
-    const float r = rsqrtf(ss * (1.0f / kUnit) + eps);  // mean: exact power-of-two scale
-    float o[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) o[e] = c[e] * r;
-    round4(ATag{}, o);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float h = gm[e] * o[e];
-      const float s = zf[e] / (1.0f + expf(-zf[e]));
-      o[e] = h * s;
+    if (lb) {
+      load4(YTag{}, y, ib, cb);
+      load4(ATag{}, z, ib, zb);
     }
-    if (live) {
-      round_store4(ATag{}, core, i, o);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) m = nan_max(m, fabsf(o[e]));
-    }
+    gated_unit<ATag>(ca, za, gm, eps, la, core, ia, m);
+    if (u0 + step < units) gated_unit<ATag>(cb, zb, gm, eps, lb, core, ib, m);
   }
   m = block_nan_max(m);
   if (partial != nullptr && threadIdx.x == 0) partial[blockIdx.x] = m;

@@ -101,6 +101,10 @@ __device__ __forceinline__ float quant_value(float x, float sc) {
   return v;
 }
 
+// Vectors each thread keeps in flight per grid-stride step: four 16-byte loads
+// are issued before any of them is used.
+constexpr int kUnroll = 4;
+
 template <class Tag>
 __global__ void __launch_bounds__(kThreads)
 amax_partial(const typename Tag::T* __restrict__ x, float* __restrict__ partial, long n,
@@ -111,7 +115,18 @@ amax_partial(const typename Tag::T* __restrict__ x, float* __restrict__ partial,
   long tail = 0;
   if (vec) {
     const long nv = n / kVec;
-    for (long j = tid; j < nv; j += stride) {
+    long j = tid;
+    for (; j + (kUnroll - 1) * stride < nv; j += kUnroll * stride) {
+      float o[kUnroll][kVec];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) load_vec(Tag{}, x, (j + u * stride) * kVec, o[u]);
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+#pragma unroll
+        for (int e = 0; e < kVec; ++e) m = nan_max(m, fabsf(o[u][e]));
+      }
+    }
+    for (; j < nv; j += stride) {
       float o[kVec];
       load_vec(Tag{}, x, j * kVec, o);
 #pragma unroll
@@ -124,10 +139,40 @@ amax_partial(const typename Tag::T* __restrict__ x, float* __restrict__ partial,
   if (threadIdx.x == 0) partial[blockIdx.x] = m;
 }
 
+__device__ __forceinline__ uint2 quant_vec(const float (&o)[kVec], float sc) {
+  uint32_t lo = 0, hi = 0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    lo |= e4m3fn_code(quant_value(o[e], sc)) << (8 * e);
+    hi |= e4m3fn_code(quant_value(o[e + 4], sc)) << (8 * e);
+  }
+  return make_uint2(lo, hi);
+}
+
+// Eight codes, one 8-byte nontemporal store (the codes are read once, by the
+// GEMM that consumes them).
+__device__ __forceinline__ void store_codes(uint8_t* p, uint2 v) {
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  __builtin_nontemporal_store((u32x2){v.x, v.y}, reinterpret_cast<u32x2*>(p));
+}
+
+// The first grid-stride step's loads are issued before the partials are
+// reduced to the scale, so the reduction overlaps them.
 template <class Tag>
 __global__ void __launch_bounds__(kThreads)
 quantize(const typename Tag::T* __restrict__ x, const float* __restrict__ partial, int nparts,
          float* __restrict__ scale, uint8_t* __restrict__ q, long n, int vec) {
+  const long tid = (long)blockIdx.x * kThreads + threadIdx.x;
+  const long stride = (long)gridDim.x * kThreads;
+  const long nv = vec ? n / kVec : 0;
+  float o[kUnroll][kVec];
+  long j = tid;
+  bool full = j + (kUnroll - 1) * stride < nv;
+  if (full) {
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) load_vec(Tag{}, x, (j + u * stride) * kVec, o[u]);
+  }
+
   float m = 0.f;
   for (int i = threadIdx.x; i < nparts; i += kThreads) m = nan_max(m, partial[i]);
   m = block_nan_max(m);
@@ -135,25 +180,23 @@ quantize(const typename Tag::T* __restrict__ x, const float* __restrict__ partia
   const float sc = (raw < kEps) ? kEps : raw;
   if (blockIdx.x == 0 && threadIdx.x == 0) scale[0] = sc;
 
-  const long tid = (long)blockIdx.x * kThreads + threadIdx.x;
-  const long stride = (long)gridDim.x * kThreads;
-  long tail = 0;
-  if (vec) {
-    const long nv = n / kVec;
-    for (long j = tid; j < nv; j += stride) {
-      float o[kVec];
-      load_vec(Tag{}, x, j * kVec, o);
-      uint32_t lo = 0, hi = 0;
+  while (full) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        lo |= e4m3fn_code(quant_value(o[e], sc)) << (8 * e);
-        hi |= e4m3fn_code(quant_value(o[e + 4], sc)) << (8 * e);
-      }
-      *reinterpret_cast<uint2*>(q + j * kVec) = make_uint2(lo, hi);
+    for (int u = 0; u < kUnroll; ++u)
+      store_codes(q + (j + u * stride) * kVec, quant_vec(o[u], sc));
+    j += kUnroll * stride;
+    full = j + (kUnroll - 1) * stride < nv;
+    if (full) {
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) load_vec(Tag{}, x, (j + u * stride) * kVec, o[u]);
     }
-    tail = nv * kVec;
   }
-  for (long i = tail + tid; i < n; i += stride)
+  for (; j < nv; j += stride) {
+    float v1[kVec];
+    load_vec(Tag{}, x, j * kVec, v1);
+    store_codes(q + j * kVec, quant_vec(v1, sc));
+  }
+  for (long i = nv * kVec + tid; i < n; i += stride)
     q[i] = (uint8_t)e4m3fn_code(quant_value(widen(Tag{}, x[i]), sc));
 }
 
