@@ -399,6 +399,7 @@ def measure_paths(torch, kern):
 
         entry = {"graph_us": round(graph_time(torch, tick_fn, reps=5,
                                               before_replay=lambda: sl.copy_(padded)) * 1e6, 1)}
+        sl.copy_(torch.arange(bucket, dtype=torch.int32, device=dev))
         if bucket <= 96:  # eager needs distinct slots (no scratch padding)
             tick_fn()
             torch.cuda.synchronize()
