@@ -129,54 +129,88 @@ gdn_conv_decode_kernel(typename Storage<Tag>::T* __restrict__ pool,
 //   v    the value row [kHD];
 //   gate alpha, beta.
 constexpr int kStage = 32;
-struct StageLds {
+struct alignas(16) StageLds {
   float qk[kStage][2][kSS];
   float v[kStage][kHD];
   float gate[kStage][2];
 };
 
-// Fills `st` for tokens [t0, t0 + n) of row b, head h. Gates: one thread per
-// token, the policy's own arithmetic. q and k: each wave takes every
-// (waves)-th token, two at a time so the butterflies overlap, and computes the
-// norm factor with the decode's butterfly (inv_norm) and q_hat = q * factor as
-// decode's scale_qk does: the same bits. v: 16-byte copies.
+// One thread's share of a stage's global inputs, loaded a whole stage ahead so
+// that the loads are in flight while the previous stage's serial loop runs:
+// wave w holds tokens w, w + waves, ... (q and k as the float2 pair each lane
+// reduces for the norms), and every thread kV4 of the stage's 16-byte v pieces
+// and (thread j < kStage) token j's raw gate values.
+template <int kTileWaves>
+struct StageRegs {
+  static constexpr int kTok = kStage / kTileWaves;
+  static constexpr int kV4 = kStage * (kHD / 4) / (64 * kTileWaves);
+  float2 q[kTok], k[kTok];
+  float4 v[kV4];
+  GateRaw gate;
+};
+
 template <int kTileWaves, class Gates>
-__device__ __forceinline__ void scan_stage_prologue(int wave, int lane, const Gates& gates,
-                                                    const float* __restrict__ q,
-                                                    const float* __restrict__ k,
-                                                    const float* __restrict__ v, int b, int h,
-                                                    int g, int H, int G, int T, int t0, int n,
-                                                    StageLds& st) {
+__device__ __forceinline__ void load_stage(StageRegs<kTileWaves>& r, int wave, int lane,
+                                           const Gates& gates, const float* __restrict__ q,
+                                           const float* __restrict__ k,
+                                           const float* __restrict__ v, int b, int h, int g,
+                                           int H, int G, int T, int t0, int n) {
   constexpr int kThreads = 64 * kTileWaves;
-  for (int j = threadIdx.x; j < n; j += kThreads) {
-    const GateRaw r = gates.load(b, h, t0 + j, H, T);
-    st.gate[j][0] = gates.eval_alpha(r, h);
-    st.gate[j][1] = gates.eval_beta(r);
+  if ((int)threadIdx.x < n) r.gate = gates.load(b, h, t0 + threadIdx.x, H, T);
+#pragma unroll
+  for (int m = 0; m < StageRegs<kTileWaves>::kV4; ++m) {
+    const int e = threadIdx.x + m * kThreads, j = e / (kHD / 4), c4 = e % (kHD / 4);
+    if (j < n)
+      r.v[m] = *reinterpret_cast<const float4*>(v + (((size_t)b * T + t0 + j) * H + h) * kHD +
+                                                4 * c4);
   }
-  constexpr int kV4 = kHD / 4;
-  for (int e = threadIdx.x; e < n * kV4; e += kThreads) {
-    const int j = e / kV4, c4 = e % kV4;
-    *reinterpret_cast<float4*>(&st.v[j][4 * c4]) =
-        *reinterpret_cast<const float4*>(v + (((size_t)b * T + t0 + j) * H + h) * kHD + 4 * c4);
-  }
-  for (int j = wave; j < n; j += 2 * kTileWaves) {
-    const int j2 = j + kTileWaves;
-    const size_t o1 = (((size_t)b * T + t0 + j) * G + g) * kSS + 2 * lane;
-    const float2 q1 = *reinterpret_cast<const float2*>(q + o1);
-    const float2 k1 = *reinterpret_cast<const float2*>(k + o1);
-    float2 q2 = make_float2(0.f, 0.f), k2 = make_float2(0.f, 0.f);
-    if (j2 < n) {
-      const size_t o2 = (((size_t)b * T + t0 + j2) * G + g) * kSS + 2 * lane;
-      q2 = *reinterpret_cast<const float2*>(q + o2);
-      k2 = *reinterpret_cast<const float2*>(k + o2);
+#pragma unroll
+  for (int m = 0; m < StageRegs<kTileWaves>::kTok; ++m) {
+    const int j = wave + m * kTileWaves;
+    if (j < n) {
+      const size_t o = (((size_t)b * T + t0 + j) * G + g) * kSS + 2 * lane;
+      r.q[m] = *reinterpret_cast<const float2*>(q + o);
+      r.k[m] = *reinterpret_cast<const float2*>(k + o);
     }
-    const float qi1 = inv_norm(q1), ki1 = inv_norm(k1);
-    const float qi2 = inv_norm(q2), ki2 = inv_norm(k2);
-    *reinterpret_cast<float2*>(&st.qk[j][0][2 * lane]) = make_float2(q1.x * qi1, q1.y * qi1);
-    *reinterpret_cast<float2*>(&st.qk[j][1][2 * lane]) = make_float2(k1.x * ki1, k1.y * ki1);
+  }
+}
+
+// Turns the prefetched inputs of tokens [t0, t0 + n) into the stage in LDS.
+// Gates: the policy's own arithmetic. q and k: the norm factor with the
+// decode's butterfly (inv_norm), two tokens at a time so the butterflies
+// overlap, and q_hat = q * factor as decode's scale_qk does: the same bits.
+template <int kTileWaves, class Gates>
+__device__ __forceinline__ void write_stage(const StageRegs<kTileWaves>& r, int wave, int lane,
+                                            const Gates& gates, int h, int n, StageLds& st) {
+  constexpr int kThreads = 64 * kTileWaves;
+  if ((int)threadIdx.x < n) {
+    st.gate[threadIdx.x][0] = gates.eval_alpha(r.gate, h);
+    st.gate[threadIdx.x][1] = gates.eval_beta(r.gate);
+  }
+#pragma unroll
+  for (int m = 0; m < StageRegs<kTileWaves>::kV4; ++m) {
+    const int e = threadIdx.x + m * kThreads, j = e / (kHD / 4), c4 = e % (kHD / 4);
+    if (j < n) *reinterpret_cast<float4*>(&st.v[j][4 * c4]) = r.v[m];
+  }
+#pragma unroll
+  for (int m = 0; m < StageRegs<kTileWaves>::kTok; m += 2) {
+    const int j = wave + m * kTileWaves, j2 = j + kTileWaves;
+    if (j >= n) break;
+    const float qi1 = inv_norm(r.q[m]), ki1 = inv_norm(r.k[m]);
+    float qi2 = 0.f, ki2 = 0.f;
     if (j2 < n) {
-      *reinterpret_cast<float2*>(&st.qk[j2][0][2 * lane]) = make_float2(q2.x * qi2, q2.y * qi2);
-      *reinterpret_cast<float2*>(&st.qk[j2][1][2 * lane]) = make_float2(k2.x * ki2, k2.y * ki2);
+      qi2 = inv_norm(r.q[m + 1]);
+      ki2 = inv_norm(r.k[m + 1]);
+    }
+    *reinterpret_cast<float2*>(&st.qk[j][0][2 * lane]) =
+        make_float2(r.q[m].x * qi1, r.q[m].y * qi1);
+    *reinterpret_cast<float2*>(&st.qk[j][1][2 * lane]) =
+        make_float2(r.k[m].x * ki1, r.k[m].y * ki1);
+    if (j2 < n) {
+      *reinterpret_cast<float2*>(&st.qk[j2][0][2 * lane]) =
+          make_float2(r.q[m + 1].x * qi2, r.q[m + 1].y * qi2);
+      *reinterpret_cast<float2*>(&st.qk[j2][1][2 * lane]) =
+          make_float2(r.k[m + 1].x * ki2, r.k[m + 1].y * ki2);
     }
   }
 }
@@ -213,9 +247,9 @@ __device__ __forceinline__ void read_token(const StageLds& st, int j, int r0, in
 // rows of its row block for two columns; the column sums finish in-lane and
 // over the four row blocks with permlane swaps, by the decode's summation
 // tree, so the bits are the decode's and no token needs a workgroup barrier.
-// Tokens run in stages of kStage: a parallel prologue stages their inputs in
-// LDS (StageLds), then the serial loop carries only the recurrence and the
-// output stores.
+// Tokens run in stages of kStage: their inputs are loaded a stage ahead
+// (StageRegs) and staged in LDS (StageLds) between stages, so the serial loop
+// carries only the recurrence and the output stores.
 template <class Tag, class Gates>
 __global__ void __launch_bounds__(64 * ScanMap<kPrefillCols>::kWavesPerTile)
 gdn_prefill_kernel(typename Storage<Tag>::T* __restrict__ pool,
@@ -243,15 +277,20 @@ gdn_prefill_kernel(typename Storage<Tag>::T* __restrict__ pool,
     for (int i = 0; i < kRowsPerLane; ++i) S[rg][i].load_nt(tile + (size_t)L.row(rg, i) * kHD);
   }
 
+  constexpr int kW = LM::kWavesPerTile;
   const int r0 = L.w * kRowsPerWave;
+  StageRegs<kW> pre;
+  load_stage<kW>(pre, L.wave, L.lane, gates, q, k, v, b, h, g, H, G, T, 0, min(kStage, T));
   for (int t0 = 0; t0 < T; t0 += kStage) {
     const int n = min(kStage, T - t0);
     // Every wave has finished reading the previous stage (the barrier at the
-    // end of the stage loop), so the prologue may overwrite it.
-    scan_stage_prologue<LM::kWavesPerTile>(L.wave, L.lane, gates, q, k, v, b, h, g, H, G, T, t0,
-                                           n, st);
+    // end of the stage loop), so it may be overwritten.
+    write_stage<kW>(pre, L.wave, L.lane, gates, h, n, st);
     __syncthreads();
-    // Token j + 1's staged inputs are read while token j computes.
+    // The next stage's loads fly while this stage's tokens run.
+    if (t0 + kStage < T)
+      load_stage<kW>(pre, L.wave, L.lane, gates, q, k, v, b, h, g, H, G, T, t0 + kStage,
+                     min(kStage, T - t0 - kStage));
     for (int j = 0; j < n; ++j) {
       TokenIn in;
       read_token(st, j, r0, L.col0, in);
