@@ -1,4 +1,4 @@
-"""``load_gdn()``: the six GDN hot-path entry points over the C ABI.
+"""``load_gdn()``: the GDN hot-path entry points over the C ABI.
 
 Drop-in for ``braid.kernels.loader.load_gdn`` (braid/kernels/loader.py:10-44),
 which JIT-built a pybind11 module exposing ``gdn_decode``, ``gdn_prefill``,
@@ -16,6 +16,12 @@ prebuilt gfx950 library ``braid_amd/libbraid_gdn.so`` (C ABI declared in
   performs (skipped while the stream is capturing a graph);
 * ``quantize_act`` allocates its outputs (and the small partial-max
   workspace) in torch, as the reference's did.
+
+Beyond the reference's six, the object fronts the rows this build adds on
+either side of the scan: ``conv1d_prefill`` (the prefill conv the reference
+ran in torch), ``gdn_conv_decode_raw`` (conv1d_decode + gdn_decode_raw in one
+launch), ``gated_rmsnorm`` (the readout and the out_proj input quantization)
+and ``fp8_matmul`` (the FP8 GEMM, hipBLASLt).
 
 There is no CPU or torch fallback: if the library is missing or a tensor is
 not on the GPU, the call raises.
