@@ -128,3 +128,29 @@ def test_row_stride_rules_match_the_reference():
                               require_cuda=False)
     with pytest.raises(RuntimeError, match="dense in its last two dims"):
         loader._row_stride_3d(torch.zeros(2, 128, 2).transpose(1, 2), "q", require_cuda=False)
+
+
+def test_added_entry_points_reject_bad_arguments_before_any_gpu_call(lib):
+    fake = ctypes.c_void_p(4096)
+    rc = lib.braid_gated_rmsnorm_quant(fake, 0, fake, 2, fake, ctypes.c_float(1e-6), 64, 64,
+                                       fake, None, None, None, None)
+    assert rc == 1 and "head_dim must be 128" in _err(lib)
+    rc = lib.braid_gated_rmsnorm_quant(fake, 0, fake, 2, fake, ctypes.c_float(1e-6), 64, 128,
+                                       fake, fake, None, None, None)
+    assert rc == 1 and "given together" in _err(lib)
+    rc = lib.braid_gated_rmsnorm_quant(fake, 0, fake, 2, fake, ctypes.c_float(1e-6), 0, 128,
+                                       fake, fake, fake, fake, None)
+    assert rc == 1 and "must not be empty" in _err(lib)
+    rc = lib.braid_gdn_conv_decode_raw(fake, 1, 16, 8, 4, 128, 128, fake, 3, fake, 2, fake, 2,
+                                       fake, None, fake, fake, 2, fake, fake, fake, None)
+    assert rc == 1 and "conv_kernel == 4" in _err(lib)
+    rc = lib.braid_gdn_conv_decode_raw(fake, 1, 16, 8, 2, 128, 128, fake, 4, fake, 2, fake, 2,
+                                       fake, None, fake, fake, 2, fake, fake, fake, None)
+    assert rc == 1 and "1 or 2 value heads" in _err(lib)
+    rc = lib.braid_fp8_gemm(fake, fake, fake, fake, fake, 2, 4, 24, 40, fake,
+                            lib.braid_fp8_gemm_workspace(), None)
+    assert rc == 1 and "multiples of 16" in _err(lib)
+    rc = lib.braid_fp8_gemm(fake, fake, fake, fake, fake, 2, 0, 32, 32, fake, 0, None)
+    assert rc == 1 and "positive" in _err(lib)
+    assert lib.braid_fp8_gemm_workspace() == 32 << 20
+    assert lib.braid_gated_rmsnorm_workspace(64 * 32) == 256
