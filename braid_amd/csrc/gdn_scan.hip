@@ -9,6 +9,8 @@
 // it back; prefill loads it once, runs T tokens with the tile resident in
 // registers (in the pool's storage type) and stores it once. Reference behaviour: braid/kernels/csrc/gdn_decode.cu:156-272 (decode)
 // and :467-551 (prefill); entry-point contracts :313-441 and :553-699.
+#include <type_traits>
+
 #include "capi_common.h"
 #include "conv_common.h"
 #include "gdn_tile.h"
@@ -75,12 +77,13 @@ struct ConvDecodeLds {
 };
 
 template <class Tag, class XT, class Gates, int HPG>
-__global__ void __launch_bounds__(tile_threads(kDecodeCols) * HPG)
-gdn_conv_decode_kernel(typename Storage<Tag>::T* __restrict__ pool,
-                       float* __restrict__ conv_pool, const int* __restrict__ slot_idx,
-                       const XT* __restrict__ x, const float* __restrict__ conv_w,
-                       const float* __restrict__ conv_b, Gates gates, float* __restrict__ y,
-                       int H, int G, int C) {
+__device__ __forceinline__ void conv_decode_body(typename Storage<Tag>::T* __restrict__ pool,
+                                                 float* __restrict__ conv_pool,
+                                                 const int* __restrict__ slot_idx,
+                                                 const XT* __restrict__ x,
+                                                 const float* __restrict__ conv_w,
+                                                 const float* __restrict__ conv_b, Gates gates,
+                                                 float* __restrict__ y, int H, int G, int C) {
   constexpr int CPL = kDecodeCols, kK = 4;
   constexpr int kTileThreads = tile_threads(CPL);
   using ST = typename Storage<Tag>::T;
@@ -93,21 +96,58 @@ gdn_conv_decode_kernel(typename Storage<Tag>::T* __restrict__ pool,
   __shared__ ConvDecodeLds<HPG> lds;
   const int slot = slot_idx[b];
   ST* tile = pool + ((size_t)slot * H + h) * (kSS * kHD) + L.col0;
-  Row<Tag, CPL> S[kRowsPerLane];
-#pragma unroll
-  for (int i = 0; i < kRowsPerLane; ++i) S[i].load_nt(tile + (size_t)L.row(i) * kHD);
 
-  // Conv for the group's channels: segment 0 = q (channels g*SS..), 1 = k
+  // The group's conv channels: segment 0 = q (channels g*SS..), 1 = k
   // (G*SS + g*SS..), 2 + j = v of head g*HPG + j (2*G*SS + head*HD..).
-  for (int e = threadIdx.x; e < (2 + HPG) * kHD; e += kTileThreads * HPG) {
+  // Loads complete in issue order, so for a 16-bit pool the conv's small loads
+  // are issued before the state's and the conv arithmetic then overlaps the
+  // state's arrival; an fp32 tile leaves no registers for that (it would
+  // spill at four waves per SIMD), so there the state is loaded first.
+  constexpr int kConv = (2 + HPG) * kHD;
+  constexpr int kThreads = kTileThreads * HPG;
+  constexpr int kPer = (kConv + kThreads - 1) / kThreads;
+  constexpr bool kConvFirst = sizeof(ST) == 2;
+  auto channel = [&](int e) {
     const int seg = e / kHD, off = e - seg * kHD;
-    const int c = seg < 2 ? seg * G * kSS + g * kSS + off
-                          : 2 * G * kSS + (g * HPG + seg - 2) * kHD + off;
-    float* st = conv_pool + ((size_t)slot * C + c) * kK;
-    float w[kK], wt[kK];
-    load_window<kK>(st, conv_w + (size_t)c * kK, w, wt);
-    lds.qkv[seg][off] = conv_step<kK>(w, conv_widen(x[(size_t)b * C + c]), wt, conv_b, c);
-    store_window<kK>(st, w);
+    return seg < 2 ? seg * G * kSS + g * kSS + off
+                   : 2 * G * kSS + (g * HPG + seg - 2) * kHD + off;
+  };
+  Row<Tag, CPL> S[kRowsPerLane];
+  if constexpr (kConvFirst) {
+    float w[kPer][kK], wt[kPer][kK], xv[kPer];
+#pragma unroll
+    for (int m = 0; m < kPer; ++m) {
+      const int e = threadIdx.x + m * kThreads;
+      if (e < kConv) {
+        const int c = channel(e);
+        load_window<kK>(conv_pool + ((size_t)slot * C + c) * kK, conv_w + (size_t)c * kK, w[m],
+                        wt[m]);
+        xv[m] = conv_widen(x[(size_t)b * C + c]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kRowsPerLane; ++i) S[i].load_nt(tile + (size_t)L.row(i) * kHD);
+#pragma unroll
+    for (int m = 0; m < kPer; ++m) {
+      const int e = threadIdx.x + m * kThreads;
+      if (e < kConv) {
+        const int c = channel(e), seg = e / kHD;
+        lds.qkv[seg][e - seg * kHD] = conv_step<kK>(w[m], xv[m], wt[m], conv_b, c);
+        store_window<kK>(conv_pool + ((size_t)slot * C + c) * kK, w[m]);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < kRowsPerLane; ++i) S[i].load_nt(tile + (size_t)L.row(i) * kHD);
+    for (int e = threadIdx.x; e < kConv; e += kThreads) {
+      const int c = channel(e), seg = e / kHD;
+      float* st = conv_pool + ((size_t)slot * C + c) * kK;
+      float w[kK], wt[kK];
+      load_window<kK>(st, conv_w + (size_t)c * kK, w, wt);
+      lds.qkv[seg][e - seg * kHD] = conv_step<kK>(w, conv_widen(x[(size_t)b * C + c]), wt,
+                                                  conv_b, c);
+      store_window<kK>(st, w);
+    }
   }
   __syncthreads();
 
@@ -121,6 +161,32 @@ gdn_conv_decode_kernel(typename Storage<Tag>::T* __restrict__ pool,
 #pragma unroll
   for (int i = 0; i < kRowsPerLane; ++i) S[i].store_nt(tile + (size_t)L.row(i) * kHD);
   if (L.stores_y()) storeN<CPL>(y + ((size_t)b * H + h) * kHD + L.col0, yy);
+}
+
+// Two entry kernels over the same body. A 16-bit pool's body fits in 128
+// VGPRs (four waves per SIMD) only when the compiler is told to aim for that
+// occupancy; an fp32 pool's body spills under that constraint and is left to
+// the default, where it also lands at 128.
+template <class Tag, class XT, class Gates, int HPG>
+__global__ void __launch_bounds__(tile_threads(kDecodeCols) * HPG)
+__attribute__((amdgpu_waves_per_eu(4)))
+gdn_conv_decode_kernel(typename Storage<Tag>::T* __restrict__ pool,
+                       float* __restrict__ conv_pool, const int* __restrict__ slot_idx,
+                       const XT* __restrict__ x, const float* __restrict__ conv_w,
+                       const float* __restrict__ conv_b, Gates gates, float* __restrict__ y,
+                       int H, int G, int C) {
+  conv_decode_body<Tag, XT, Gates, HPG>(pool, conv_pool, slot_idx, x, conv_w, conv_b, gates, y,
+                                        H, G, C);
+}
+
+template <class XT, class Gates, int HPG>
+__global__ void __launch_bounds__(tile_threads(kDecodeCols) * HPG)
+gdn_conv_decode_kernel_f32(float* __restrict__ pool, float* __restrict__ conv_pool,
+                           const int* __restrict__ slot_idx, const XT* __restrict__ x,
+                           const float* __restrict__ conv_w, const float* __restrict__ conv_b,
+                           Gates gates, float* __restrict__ y, int H, int G, int C) {
+  conv_decode_body<F32, XT, Gates, HPG>(pool, conv_pool, slot_idx, x, conv_w, conv_b, gates, y,
+                                        H, G, C);
 }
 
 // A prefill stage: the next kStage tokens' per-token inputs, staged in LDS by
@@ -516,9 +582,14 @@ void launch_conv_decode_as(void* pool, float* conv_pool, const int32_t* slot_idx
                            int G, int C, const void* x, const float* w, const float* bias,
                            Gates gates, float* y, hipStream_t stream) {
   const dim3 grid((unsigned)B * (unsigned)G), block(tile_threads(kDecodeCols) * HPG);
-  gdn_conv_decode_kernel<Tag, XT, Gates, HPG><<<grid, block, 0, stream>>>(
-      static_cast<typename Storage<Tag>::T*>(pool), conv_pool, slot_idx,
-      static_cast<const XT*>(x), w, bias, gates, y, H, G, C);
+  if constexpr (std::is_same<Tag, F32>::value)
+    gdn_conv_decode_kernel_f32<XT, Gates, HPG><<<grid, block, 0, stream>>>(
+        static_cast<float*>(pool), conv_pool, slot_idx, static_cast<const XT*>(x), w, bias,
+        gates, y, H, G, C);
+  else
+    gdn_conv_decode_kernel<Tag, XT, Gates, HPG><<<grid, block, 0, stream>>>(
+        static_cast<typename Storage<Tag>::T*>(pool), conv_pool, slot_idx,
+        static_cast<const XT*>(x), w, bias, gates, y, H, G, C);
 }
 
 template <class Tag, class XT, class Gates>
