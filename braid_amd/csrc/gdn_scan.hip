@@ -38,7 +38,9 @@ gdn_decode_kernel(typename Storage<Tag>::T* __restrict__ pool, const int* __rest
   const int slot = slot_idx[b];
   ST* tile = pool + ((size_t)slot * H + h) * (kSS * kHD) + L.col0;
 
-  // Issue the whole tile's loads first; the norms and gates below overlap them.
+  // Issue the whole tile's loads first. (Loads complete in issue order, so the
+  // norms and gates below wait for the tile; issuing the small q/k/v/gate loads
+  // ahead of it changed nothing measurable: the step is bound by the state.)
   Row<Tag, CPL> S[kRowsPerLane];
 #pragma unroll
   for (int i = 0; i < kRowsPerLane; ++i) S[i].load_nt(tile + (size_t)L.row(i) * kHD);
