@@ -17,6 +17,11 @@ Roofline: the decode is HBM-bound. Algorithmic bytes per step are
 274,744,064 (state read + write 268,435,456; q/k/v/y 6,291,456; bf16 gates
 16,384; A/dt_bias/slot map 768). achieved = bytes / mean step time; peak 8 TB/s.
 
+stream_ceiling: the same 4096 state tiles streamed in place, read only and
+written only by libbraid_probe.so at the decode's lane layout, with no
+arithmetic and no q/k/v/y traffic: the ceiling the access pattern allows on
+this box, beside the 8 TB/s datasheet peak.
+
 cpu_baseline: the CPU oracle (oracle/gdn_oracle.c, a scalar port of the same
 recurrence, one thread) timed on a bounded sample of rows of the same
 workload and scaled to steps/s at B=128.
@@ -146,6 +151,67 @@ def copy_bandwidth(torch, nbytes=2 ** 30):
     secs = start.elapsed_time(end) / 1e3 / reps
     del src, dst
     return 2 * nbytes / secs / 1e9
+
+
+def stream_ceiling(torch, n_pools, launches=256):
+    """What an in-place stream of the step's state tiles reaches on this box:
+    libbraid_probe.so's read-modify-write, read-only and write-only passes
+    over the same 4096 tiles of 32 KiB (slot-permuted, cold pools, the
+    decode's lane layout, nontemporal 128-bit accesses), without the
+    arithmetic or the q/k/v/y traffic. Captured in one graph, timed with
+    events. GB/s count the state bytes each pass moves."""
+    import ctypes
+
+    from braid_amd.build import PROBE_LIB
+
+    lib = ctypes.CDLL(str(PROBE_LIB))
+    fn = lib.braid_probe_stream
+    fn.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
+                   ctypes.c_void_p, ctypes.c_void_p]
+    fn.restype = ctypes.c_int
+    dev = "cuda"
+    pools = [torch.empty(SLOTS * H * D * D, dtype=torch.float16, device=dev)
+             for _ in range(n_pools)]
+    for p in pools:
+        p.normal_()
+    maps = []
+    for p in range(n_pools):
+        perm = torch.randperm(SLOTS, generator=torch.Generator().manual_seed(p))[:B]
+        maps.append((perm[:, None] * H + torch.arange(H)[None, :]).reshape(-1)
+                    .to(torch.int32).to(dev))
+    sink = torch.empty(1024, dtype=torch.int32, device=dev)
+    n_tiles = B * H
+    tile_bytes = D * D * 2
+    out = {}
+    for kind, label, nbytes in ((0, "rmw", 2 * n_tiles * tile_bytes),
+                                (1, "read", n_tiles * tile_bytes),
+                                (2, "write", n_tiles * tile_bytes)):
+        def launch(i):
+            st = torch.cuda.current_stream().cuda_stream
+            rc = fn(kind, pools[i % n_pools].data_ptr(), n_tiles, maps[i % n_pools].data_ptr(),
+                    sink.data_ptr(), st)
+            if rc != 0:
+                raise RuntimeError(f"braid_probe_stream failed ({rc})")
+
+        for i in range(2 * n_pools):
+            launch(i)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for i in range(launches):
+                launch(i)
+        graph.replay()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        graph.replay()
+        b.record()
+        torch.cuda.synchronize()
+        secs = a.elapsed_time(b) / 1e3 / launches
+        out[f"{label}_us"] = round(secs * 1e6, 2)
+        out[f"{label}_gbs"] = round(nbytes / secs / 1e9, 1)
+    del pools
+    return out
 
 
 def cpu_baseline(budget_s):
@@ -436,6 +502,8 @@ def main():
     del work, hot_work
     torch.cuda.empty_cache()
     copy_gbs = copy_bandwidth(torch)
+    ceiling = stream_ceiling(torch, n_cold)
+    torch.cuda.empty_cache()
 
     step_s = t_cold / args.steps
     achieved = STEP_BYTES / step_s / 1e9
@@ -468,6 +536,10 @@ def main():
         "hot_achieved_gbs": round(STEP_BYTES / (t_hot / args.steps) / 1e9, 1),
         "copy_gbs": round(copy_gbs, 1),
         "bytes_per_step": STEP_BYTES,
+        # the same tiles streamed in place with no arithmetic and no q/k/v/y
+        # (libbraid_probe.so); decode_vs_rmw = probe time / decode time
+        "stream_ceiling": dict(ceiling, decode_vs_rmw=round(ceiling["rmw_us"] / (step_s * 1e6),
+                                                            4)),
     }
     if not args.no_paths:
         out["paths"] = measure_paths(torch, kern)

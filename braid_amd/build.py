@@ -27,6 +27,10 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 ROOT = PKG.parent
 LIB = PKG / "libbraid_gdn.so"
+# The HBM stream probe bench.py measures the roofline ceiling with; not part
+# of the drop-in ABI.
+PROBE_LIB = PKG / "libbraid_probe.so"
+PROBE_SOURCE = "hbm_probe.hip"
 OBJ_DIR = PKG / "_build"
 
 SOURCES = ["capi_common.cpp", "gdn_scan.hip", "conv1d_decode.hip", "quant_act.hip",
@@ -83,7 +87,23 @@ def build(verbose: bool = False, defines: tuple = (), lib: Path = LIB) -> Path:
     os.replace(tmp, lib)
     if verbose:
         print(f"built {lib}")
+    if lib == LIB:
+        build_probe(verbose)
     return lib
+
+
+def build_probe(verbose: bool = False) -> Path:
+    """Compile and link libbraid_probe.so (the HBM stream probe)."""
+    obj = _compile(PROBE_SOURCE)
+    tmp = PROBE_LIB.with_suffix(".so.tmp")
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", str(obj), "-o", str(tmp)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link failed:\n{' '.join(cmd)}\n{r.stdout}{r.stderr}")
+    os.replace(tmp, PROBE_LIB)
+    if verbose:
+        print(f"built {PROBE_LIB}")
+    return PROBE_LIB
 
 
 if __name__ == "__main__":

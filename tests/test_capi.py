@@ -154,3 +154,25 @@ def test_added_entry_points_reject_bad_arguments_before_any_gpu_call(lib):
     assert rc == 1 and "positive" in _err(lib)
     assert lib.braid_fp8_gemm_workspace() == 32 << 20
     assert lib.braid_gated_rmsnorm_workspace(64 * 32) == 256
+
+
+def test_stream_probe_library_loads_and_rejects_bad_arguments():
+    """libbraid_probe.so (bench.py's roofline ceiling, outside the drop-in
+    ABI) exports braid_probe_stream and refuses bad arguments before any GPU
+    call."""
+    import ctypes
+
+    from braid_amd.build import PROBE_LIB
+
+    if not PROBE_LIB.exists():
+        pytest.skip("libbraid_probe.so not built")
+    lib = ctypes.CDLL(str(PROBE_LIB))
+    fn = lib.braid_probe_stream
+    fn.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
+                   ctypes.c_void_p, ctypes.c_void_p]
+    fn.restype = ctypes.c_int
+    dummy = ctypes.c_void_p(16)
+    assert fn(0, None, 4, dummy, None, None) != 0      # null base
+    assert fn(0, dummy, 0, dummy, None, None) != 0     # no tiles
+    assert fn(3, dummy, 4, dummy, None, None) != 0     # unknown kind
+    assert fn(1, dummy, 4, dummy, None, None) != 0     # read pass without a sink

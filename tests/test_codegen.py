@@ -19,7 +19,7 @@ import pytest
 
 from braid_amd import build as B
 
-SOURCES = ["gdn_scan.hip", "conv1d_decode.hip", "quant_act.hip", "gated_norm.hip"]
+SOURCES = ["gdn_scan.hip", "conv1d_decode.hip", "quant_act.hip", "gated_norm.hip", "hbm_probe.hip"]
 
 
 @pytest.fixture(scope="module")
