@@ -9,6 +9,7 @@
 // it back; prefill loads it once, runs T tokens with the tile resident in
 // registers (in the pool's storage type) and stores it once. Reference behaviour: braid/kernels/csrc/gdn_decode.cu:156-272 (decode)
 // and :467-551 (prefill); entry-point contracts :313-441 and :553-699.
+#include <cstdlib>
 #include <type_traits>
 
 #include "capi_common.h"
@@ -284,14 +285,16 @@ __device__ __forceinline__ void write_stage(const StageRegs<kTileWaves>& r, int 
 }
 
 // One token's inputs for a lane of the scan layout, read from the stage.
+template <int CPL>
 struct TokenIn {
   float kh[kRowsPerWave], qh[kRowsPerWave];  // the lane's row block, row order
-  float v[kPrefillCols];
+  float v[CPL];
   float alpha, beta;
 };
 
+template <int CPL>
 __device__ __forceinline__ void read_token(const StageLds& st, int j, int r0, int col0,
-                                           TokenIn& t) {
+                                           TokenIn<CPL>& t) {
   typedef float f32x4 __attribute__((ext_vector_type(4)));
 #pragma unroll
   for (int r = 0; r < kRowsPerWave; r += 4) {
@@ -303,9 +306,14 @@ __device__ __forceinline__ void read_token(const StageLds& st, int j, int r0, in
       t.qh[r + e] = q4[e];
     }
   }
-  const float2 v2 = *reinterpret_cast<const float2*>(&st.v[j][col0]);
-  t.v[0] = v2.x;
-  t.v[1] = v2.y;
+  if constexpr (CPL == 2) {
+    const float2 v2 = *reinterpret_cast<const float2*>(&st.v[j][col0]);
+    t.v[0] = v2.x;
+    t.v[1] = v2.y;
+  } else {
+    static_assert(CPL == 1, "one or two columns per lane");
+    t.v[0] = st.v[j][col0];
+  }
   t.alpha = st.gate[j][0];
   t.beta = st.gate[j][1];
 }
@@ -318,21 +326,21 @@ __device__ __forceinline__ void read_token(const StageLds& st, int j, int r0, in
 // Tokens run in stages of kStage: their inputs are loaded a stage ahead
 // (StageRegs) and staged in LDS (StageLds) between stages, so the serial loop
 // carries only the recurrence and the output stores.
-template <class Tag, class Gates>
-__global__ void __launch_bounds__(64 * ScanMap<kPrefillCols>::kWavesPerTile)
+template <class Tag, class Gates, int CPL>
+__global__ void __launch_bounds__(64 * ScanMap<CPL>::kWaves)
 gdn_prefill_kernel(typename Storage<Tag>::T* __restrict__ pool,
                    const int* __restrict__ slot_idx,
                    const float* __restrict__ q, const float* __restrict__ k,
                    const float* __restrict__ v, Gates gates, float* __restrict__ y,
                    int H, int G, int heads_per_group, int T) {
-  constexpr int CPL = kPrefillCols;
-  static_assert(CPL == 2, "the staged v entries are read as one 8-byte vector per lane");
   using LM = ScanMap<CPL>;
   using ST = typename Storage<Tag>::T;
-  const int b = blockIdx.x / H;
-  const int h = blockIdx.x - b * H;
+  const int tile_id = blockIdx.x / LM::kParts;
+  const int part = blockIdx.x - tile_id * LM::kParts;
+  const int b = tile_id / H;
+  const int h = tile_id - b * H;
   const int g = h / heads_per_group;
-  const LM L(threadIdx.x);
+  const LM L(threadIdx.x, part);
 
   __shared__ StageLds st;
   const int slot = slot_idx[b];
@@ -345,7 +353,7 @@ gdn_prefill_kernel(typename Storage<Tag>::T* __restrict__ pool,
     for (int i = 0; i < kRowsPerLane; ++i) S[rg][i].load_nt(tile + (size_t)L.row(rg, i) * kHD);
   }
 
-  constexpr int kW = LM::kWavesPerTile;
+  constexpr int kW = LM::kWaves;
   const int r0 = L.w * kRowsPerWave;
   StageRegs<kW> pre;
   load_stage<kW>(pre, L.wave, L.lane, gates, q, k, v, b, h, g, H, G, T, 0, min(kStage, T));
@@ -360,8 +368,8 @@ gdn_prefill_kernel(typename Storage<Tag>::T* __restrict__ pool,
       load_stage<kW>(pre, L.wave, L.lane, gates, q, k, v, b, h, g, H, G, T, t0 + kStage,
                      min(kStage, T - t0 - kStage));
     for (int j = 0; j < n; ++j) {
-      TokenIn in;
-      read_token(st, j, r0, L.col0, in);
+      TokenIn<CPL> in;
+      read_token<CPL>(st, j, r0, L.col0, in);
       float yy[CPL];
       scan_token<Tag, CPL>(S, in.kh, in.qh, in.v, in.alpha, in.beta, yy);
       if (L.stores_y()) storeN<CPL>(y + (((size_t)b * T + t0 + j) * H + h) * kHD + L.col0, yy);
@@ -438,26 +446,52 @@ int launch_decode(void* pool, int pool_dtype, const int32_t* slot_idx, int B, in
   return st != BRAID_OK ? st : ok();
 }
 
+// Columns per lane of a prefill launch: one (two workgroups per tile, each
+// wave carrying half the per-token work) when that still leaves no CU with a
+// second workgroup, else two. BRAID_PREFILL_COLS (1 or 2) overrides it.
+int prefill_cols(int n_tiles) {
+  const char* env = std::getenv("BRAID_PREFILL_COLS");
+  if (env != nullptr && (std::atoi(env) == 1 || std::atoi(env) == 2)) return std::atoi(env);
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return 2;
+  return 2 * n_tiles <= cus ? 1 : 2;
+}
+
+template <class Gates, int CPL>
+void launch_prefill_cols(void* pool, int pool_dtype, const int32_t* slot_idx, int B, int T,
+                         int H, int G, const float* q, const float* k, const float* v,
+                         Gates gates, float* y, hipStream_t stream) {
+  using LM = ScanMap<CPL>;
+  const dim3 grid((unsigned)B * (unsigned)H * LM::kParts), block(64 * LM::kWaves);
+  const int hpg = H / G;
+  switch (pool_dtype) {
+    case BRAID_F32:
+      gdn_prefill_kernel<F32, Gates, CPL><<<grid, block, 0, stream>>>(
+          static_cast<float*>(pool), slot_idx, q, k, v, gates, y, H, G, hpg, T);
+      break;
+    case BRAID_F16:
+      gdn_prefill_kernel<F16, Gates, CPL><<<grid, block, 0, stream>>>(
+          static_cast<uint16_t*>(pool), slot_idx, q, k, v, gates, y, H, G, hpg, T);
+      break;
+    default:
+      gdn_prefill_kernel<BF16, Gates, CPL><<<grid, block, 0, stream>>>(
+          static_cast<uint16_t*>(pool), slot_idx, q, k, v, gates, y, H, G, hpg, T);
+      break;
+  }
+}
+
 template <class Gates>
 int launch_prefill(void* pool, int pool_dtype, const int32_t* slot_idx, int B, int T, int H,
                    int G, const float* q, const float* k, const float* v, Gates gates,
                    float* y, hipStream_t stream) {
-  const dim3 grid((unsigned)B * (unsigned)H), block(64 * ScanMap<kPrefillCols>::kWavesPerTile);
-  const int hpg = H / G;
-  switch (pool_dtype) {
-    case BRAID_F32:
-      gdn_prefill_kernel<F32, Gates><<<grid, block, 0, stream>>>(
-          static_cast<float*>(pool), slot_idx, q, k, v, gates, y, H, G, hpg, T);
-      break;
-    case BRAID_F16:
-      gdn_prefill_kernel<F16, Gates><<<grid, block, 0, stream>>>(
-          static_cast<uint16_t*>(pool), slot_idx, q, k, v, gates, y, H, G, hpg, T);
-      break;
-    default:
-      gdn_prefill_kernel<BF16, Gates><<<grid, block, 0, stream>>>(
-          static_cast<uint16_t*>(pool), slot_idx, q, k, v, gates, y, H, G, hpg, T);
-      break;
-  }
+  if (prefill_cols(B * H) == 1)
+    launch_prefill_cols<Gates, 1>(pool, pool_dtype, slot_idx, B, T, H, G, q, k, v, gates, y,
+                                  stream);
+  else
+    launch_prefill_cols<Gates, 2>(pool, pool_dtype, slot_idx, B, T, H, G, q, k, v, gates, y,
+                                  stream);
   const int st = hip_status(hipGetLastError(), "launching gdn_prefill_kernel");
   return st != BRAID_OK ? st : ok();
 }

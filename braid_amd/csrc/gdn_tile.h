@@ -24,11 +24,10 @@
 //      (w0 + w1) + (w2 + w3), evaluated the same way by every lane that needs
 //      the total.
 //
-// Prefill layout (4 columns per lane): the same rows, chains, butterflies and
-// tree, with each tile's columns split across two groups of four waves (512
-// threads). A column's arithmetic does not depend on which lane holds it, so
-// the results are the decode layout's bits, while each wave does half the
-// serial per-token work.
+// Prefill layout (ScanMap: 2 columns per lane, or 1 for small launches, whose
+// tiles are then split over two workgroups): the same rows, chains and tree.
+// A column's arithmetic does not depend on which lane holds it, so the results
+// are the decode layout's bits.
 //
 // The state lives in registers in its STORAGE type. Each token widens it to
 // fp32, runs the recurrence in fp32 and narrows it back, exactly as a decode
@@ -172,6 +171,43 @@ struct Row<BF16, N> : RowHalf<N> {
   }
 };
 
+// One column per lane (the split prefill layout). The 16-bit rows keep their
+// element in the low half of a 32-bit register and narrow through the same
+// packed conversion as the pairs (the high half is discarded), so the
+// rounding is the pairs' bit for bit and the compiler cannot fuse it into the
+// producing fma.
+template <>
+struct Row<F32, 1> {
+  float d;
+  __device__ __forceinline__ void load_nt(const float* p) { d = __builtin_nontemporal_load(p); }
+  __device__ __forceinline__ void store_nt(float* p) const { __builtin_nontemporal_store(d, p); }
+  __device__ __forceinline__ float get(int) const { return d; }
+  __device__ __forceinline__ void set1(float x) { d = x; }
+};
+
+struct RowHalf1 {
+  uint32_t raw;  // the element in bits 0..15
+  __device__ __forceinline__ void load_nt(const uint16_t* p) {
+    raw = __builtin_nontemporal_load(p);
+  }
+  __device__ __forceinline__ void store_nt(uint16_t* p) const {
+    __builtin_nontemporal_store((uint16_t)raw, p);
+  }
+  __device__ __forceinline__ uint32_t bits(int) const { return raw & 0xffffu; }
+};
+
+template <>
+struct Row<F16, 1> : RowHalf1 {
+  __device__ __forceinline__ float get(int c) const { return f16_widen(bits(c)); }
+  __device__ __forceinline__ void set1(float x) { raw = pack_f16x2(x, 0.f) & 0xffffu; }
+};
+
+template <>
+struct Row<BF16, 1> : RowHalf1 {
+  __device__ __forceinline__ float get(int c) const { return bf16_widen(bits(c)); }
+  __device__ __forceinline__ void set1(float x) { raw = pack_bf16x2(x, 0.f) & 0xffffu; }
+};
+
 // ---------------------------------------------------------------------------
 // Cross-lane sums. Butterflies over lane-index bits: partners add the same two
 // operands (a + b == b + a), so after every stage all lanes of a group hold
@@ -305,17 +341,25 @@ struct LaneMap {
 // (rg0 + rg1) + (rg2 + rg3) like the decode's lane-xor-16 / xor-32 stages, and
 // the row blocks as (w0 + w1) + (w2 + w3) like the decode's LDS tree: every
 // sum has the decode's bits.
+//
+// A workgroup is four waves. With two columns per lane they own the tile's
+// 128 columns; with one column per lane (kParts = 2) a tile is two
+// workgroups, `part` owning columns [64 part, 64 part + 64). Columns never
+// meet in the recurrence, so the split changes no bit, and each wave carries
+// half the per-token work.
 template <int CPL>
 struct ScanMap {
   static constexpr int kColsPerWave = 16 * CPL;
   static constexpr int kWavesPerTile = kHD / kColsPerWave;
+  static constexpr int kWaves = 4;  // per workgroup
+  static constexpr int kParts = kWavesPerTile / kWaves;
   int wave, lane, cc, w, col0;
-  __device__ __forceinline__ ScanMap(int tid) {
+  __device__ __forceinline__ ScanMap(int tid, int part) {
     lane = tid & 63;
     wave = tid >> 6;
     cc = lane & 15;
     w = lane >> 4;
-    col0 = wave * kColsPerWave + cc * CPL;
+    col0 = (part * kWaves + wave) * kColsPerWave + cc * CPL;
   }
   __device__ __forceinline__ int row(int rg, int i) const {
     return w * kRowsPerWave + rg + kRowGroups * i;
@@ -540,13 +584,19 @@ __device__ __forceinline__ void scan_token(Row<Tag, CPL> (&S)[kRowGroups][kRowsP
 #pragma unroll
     for (int i = 0; i < kRowsPerLane; ++i) {
       const int r = rg + kRowGroups * i;
+      if constexpr (CPL == 1) {
+        const float n0 = fmaf(alpha, S[rg][i].get(0), kh[r] * delta[0]);
+        S[rg][i].set1(n0);
+        ch[rg][0] = fmaf(n0, qh[r], ch[rg][0]);
+      } else {
 #pragma unroll
-      for (int c = 0; c < CPL; c += 2) {
-        const float n0 = fmaf(alpha, S[rg][i].get(c), kh[r] * delta[c]);
-        const float n1 = fmaf(alpha, S[rg][i].get(c + 1), kh[r] * delta[c + 1]);
-        S[rg][i].set2(c, n0, n1);
-        ch[rg][c] = fmaf(n0, qh[r], ch[rg][c]);
-        ch[rg][c + 1] = fmaf(n1, qh[r], ch[rg][c + 1]);
+        for (int c = 0; c < CPL; c += 2) {
+          const float n0 = fmaf(alpha, S[rg][i].get(c), kh[r] * delta[c]);
+          const float n1 = fmaf(alpha, S[rg][i].get(c + 1), kh[r] * delta[c + 1]);
+          S[rg][i].set2(c, n0, n1);
+          ch[rg][c] = fmaf(n0, qh[r], ch[rg][c]);
+          ch[rg][c + 1] = fmaf(n1, qh[r], ch[rg][c + 1]);
+        }
       }
     }
   }
