@@ -232,3 +232,35 @@ def test_identity_steps_are_exact_up_to_the_sign_of_zero(kern, dt):
                             inp["k"][:1, t].contiguous(), inp["v"][:1, t].contiguous(),
                             a_raw[:1, t].contiguous(), b_raw[:1, t].contiguous(), A, dt_bias, o)
     assert torch.equal(pr, pd) and _same_up_to_zero_sign(pr, pd, dt)
+
+
+@pytest.mark.parametrize("cols", ["1", "2"], ids=["split-1col", "whole-2col"])
+@pytest.mark.parametrize("dt", POOL_DTYPES, ids=POOL_IDS)
+def test_both_scan_layouts_are_decode_bit_for_bit(kern, monkeypatch, dt, cols):
+    """The launch picks one column per lane (a tile split over two workgroups)
+    for small launches and two otherwise (BRAID_PREFILL_COLS forces either).
+    Both must equal decode applied T times, with raw gates and ragged
+    seq_lens, on every pool type; the automatic choice of one batch size
+    would otherwise leave the other layout untested."""
+    monkeypatch.setenv("BRAID_PREFILL_COLS", cols)
+    B, T, H, G = 3, 40, 32, 16
+    inp = prefill_inputs(B, T, H=H, G=G, seed=21)
+    a, b, A, dtb = raw_gates((B, T, H), H, torch.bfloat16, seed=22)
+    lens = torch.tensor([40, 0, 23], dtype=torch.int32, device=DEV)
+    slots = torch.tensor([5, 1, 3], dtype=torch.int32, device=DEV)
+    pc = pool(7, H=H, dtype=dt)
+    ps = pc.clone()
+    yc = torch.empty(B, T, H, 128, device=DEV)
+    kern.gdn_prefill_raw(pc, slots, inp["q"], inp["k"], inp["v"], a, b, A, dtb, yc, lens)
+    for t in range(T):
+        live = (t < lens).nonzero().flatten()
+        if live.numel() == 0:
+            continue
+        yt = torch.empty(live.numel(), H, 128, device=DEV)
+        kern.gdn_decode_raw(ps, slots[live].contiguous(), inp["q"][live, t].contiguous(),
+                            inp["k"][live, t].contiguous(), inp["v"][live, t].contiguous(),
+                            a[live, t].contiguous(), b[live, t].contiguous(), A, dtb, yt)
+        assert torch.equal(yc[live, t], yt), f"token {t}: outputs differ"
+    torch.cuda.synchronize()
+    same = (pc == ps) | (pc.isnan() & ps.isnan())
+    assert bool(same.all()), f"states differ by {(pc.float() - ps.float()).abs().max().item():.3e}"
