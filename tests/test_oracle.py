@@ -386,3 +386,42 @@ def test_gated_rmsnorm_scale_invariance_and_gate_limits():
     zf = oracle.widen(z, "bf16")
     nz = core != 0
     assert (np.sign(core[nz]) == np.sign(y[nz] * zf[nz])).all()
+
+
+def test_torch_cpu_restatement_matches_the_c_oracle():
+    """oracle/torch_ref.py (the CPU baseline bench.py times) restates the
+    reference's batched torch step; it must agree with the pinned C oracle to
+    the recurrence tolerance, state and outputs, on an fp16 pool with raw bf16
+    gates."""
+    import torch
+
+    from oracle import torch_ref
+
+    rng = np.random.default_rng(5)
+    B, H, G, D, S = 3, 32, 16, 128, 6
+    pool32 = (rng.standard_normal((S, H, D, D)) * 0.02).astype(np.float32)
+    pool16 = pool32.astype(np.float16)
+    slots = np.array([4, 0, 2], dtype=np.int32)
+    q = rng.standard_normal((B, G, D)).astype(np.float32)
+    k = rng.standard_normal((B, G, D)).astype(np.float32)
+    v = rng.standard_normal((B, H, D)).astype(np.float32)
+    a = oracle.bf16_bits(rng.standard_normal((B, H)).astype(np.float32))
+    b = oracle.bf16_bits(rng.standard_normal((B, H)).astype(np.float32))
+    A = -np.exp(rng.uniform(0, 2, H)).astype(np.float32)
+    dtb = rng.uniform(-1, 1, H).astype(np.float32)
+
+    al, be = oracle.gdn_gates(a, b, A, dtb, "bf16")
+    ref_pool = pool16.copy()
+    y_ref = oracle.gdn_decode(ref_pool, slots, q, k, v, al, be, "f16")
+
+    tp = torch.from_numpy(pool16.copy())
+    to_bf16 = lambda bits: torch.from_numpy(bits.astype(np.int16)).view(torch.bfloat16)
+    y = torch_ref.decode_step(tp, torch.from_numpy(slots), torch.from_numpy(q),
+                              torch.from_numpy(k), torch.from_numpy(v), to_bf16(a), to_bf16(b),
+                              torch.from_numpy(A), torch.from_numpy(dtb))
+    np.testing.assert_allclose(y.numpy(), y_ref, rtol=2e-5, atol=2e-6)
+    ulp = np.abs(tp.numpy().view(np.int16).astype(np.int32)
+                 - ref_pool.view(np.int16).astype(np.int32))
+    assert ulp.max() <= 1
+    untouched = [1, 3, 5]
+    assert np.array_equal(tp.numpy()[untouched], pool16[untouched])
