@@ -318,31 +318,34 @@ __device__ __forceinline__ void read_token(const StageLds& st, int j, int r0, in
   t.beta = st.gate[j][1];
 }
 
-// T tokens for the tile with the state resident in registers. Scan layout
-// (ScanMap): four waves, each owning 32 whole columns, a lane holding the 32
-// rows of its row block for two columns; the column sums finish in-lane and
-// over the four row blocks with permlane swaps, by the decode's summation
-// tree, so the bits are the decode's and no token needs a workgroup barrier.
-// Tokens run in stages of kStage: their inputs are loaded a stage ahead
-// (StageRegs) and staged in LDS (StageLds) between stages, so the serial loop
-// carries only the recurrence and the output stores.
+// The live tokens of one tile, with the state resident in registers. Scan
+// layout (ScanMap): four waves; a lane holds the 32 rows of its row block for
+// CPL columns; the column sums finish in-lane and over the four row blocks
+// with permlane swaps, by the decode's summation tree, so the bits are the
+// decode's and no token needs a workgroup barrier. Tokens run in stages of
+// kStage: their inputs are loaded a stage ahead (StageRegs) and staged in LDS
+// (StageLds) between stages, so the serial loop carries only the recurrence
+// and the output stores.
+//
+// Only the row's live tokens [0, len) run: a pad token (alpha = 1, beta = 0)
+// is an identity on the state, so skipping it leaves the state exactly as the
+// reference's pad steps do (gdn.py:301-316), up to their turning a -0 entry
+// into +0. y at the pad positions [len, T) is written as 0 (the reference
+// leaves arbitrary values there that nothing reads; zeros also keep a later
+// per-tensor FP8 scale of the readout independent of the pads).
 template <class Tag, class Gates, int CPL>
-__global__ void __launch_bounds__(64 * ScanMap<CPL>::kWaves)
-gdn_prefill_kernel(typename Storage<Tag>::T* __restrict__ pool,
-                   const int* __restrict__ slot_idx,
-                   const float* __restrict__ q, const float* __restrict__ k,
-                   const float* __restrict__ v, Gates gates, float* __restrict__ y,
-                   int H, int G, int heads_per_group, int T) {
+__device__ __forceinline__ void prefill_tile(typename Storage<Tag>::T* __restrict__ pool,
+                                             const int* __restrict__ slot_idx,
+                                             const float* __restrict__ q,
+                                             const float* __restrict__ k,
+                                             const float* __restrict__ v, const Gates& gates,
+                                             float* __restrict__ y, int H, int G,
+                                             int heads_per_group, int T, int b, int h, int part,
+                                             int len, StageLds& st) {
   using LM = ScanMap<CPL>;
   using ST = typename Storage<Tag>::T;
-  const int tile_id = blockIdx.x / LM::kParts;
-  const int part = blockIdx.x - tile_id * LM::kParts;
-  const int b = tile_id / H;
-  const int h = tile_id - b * H;
   const int g = h / heads_per_group;
   const LM L(threadIdx.x, part);
-
-  __shared__ StageLds st;
   const int slot = slot_idx[b];
   ST* tile = pool + ((size_t)slot * H + h) * (kSS * kHD) + L.col0;
 
@@ -356,17 +359,18 @@ gdn_prefill_kernel(typename Storage<Tag>::T* __restrict__ pool,
   constexpr int kW = LM::kWaves;
   const int r0 = L.w * kRowsPerWave;
   StageRegs<kW> pre;
-  load_stage<kW>(pre, L.wave, L.lane, gates, q, k, v, b, h, g, H, G, T, 0, min(kStage, T));
-  for (int t0 = 0; t0 < T; t0 += kStage) {
-    const int n = min(kStage, T - t0);
+  // (Loads nothing when len == 0; a branch around it costs ~30 VGPRs.)
+  load_stage<kW>(pre, L.wave, L.lane, gates, q, k, v, b, h, g, H, G, T, 0, min(kStage, len));
+  for (int t0 = 0; t0 < len; t0 += kStage) {
+    const int n = min(kStage, len - t0);
     // Every wave has finished reading the previous stage (the barrier at the
     // end of the stage loop), so it may be overwritten.
     write_stage<kW>(pre, L.wave, L.lane, gates, h, n, st);
     __syncthreads();
     // The next stage's loads fly while this stage's tokens run.
-    if (t0 + kStage < T)
+    if (t0 + kStage < len)
       load_stage<kW>(pre, L.wave, L.lane, gates, q, k, v, b, h, g, H, G, T, t0 + kStage,
-                     min(kStage, T - t0 - kStage));
+                     min(kStage, len - t0 - kStage));
     for (int j = 0; j < n; ++j) {
       TokenIn<CPL> in;
       read_token<CPL>(st, j, r0, L.col0, in);
@@ -381,6 +385,94 @@ gdn_prefill_kernel(typename Storage<Tag>::T* __restrict__ pool,
   for (int rg = 0; rg < kRowGroups; ++rg) {
 #pragma unroll
     for (int i = 0; i < kRowsPerLane; ++i) S[rg][i].store_nt(tile + (size_t)L.row(rg, i) * kHD);
+  }
+
+  // Zeros at the pad positions, the workgroup's columns, 16 bytes per thread.
+  constexpr int kCols = LM::kWaves * LM::kColsPerWave;  // this workgroup's columns
+  constexpr int kV4 = kCols / 4;
+  const int c0 = part * kCols;
+  for (int e = threadIdx.x; e < (T - len) * kV4; e += 64 * kW) {
+    const int t = len + e / kV4, c = c0 + 4 * (e % kV4);
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    __builtin_nontemporal_store((f32x4){0.f, 0.f, 0.f, 0.f},
+                                reinterpret_cast<f32x4*>(y + (((size_t)b * T + t) * H + h) * kHD + c));
+  }
+}
+
+// One tile (CPL = 2) or one half tile (CPL = 1, kParts = 2) per workgroup:
+// blockIdx.x = (b * H + h) * kParts + part.
+template <class Tag, class Gates, int CPL>
+__global__ void __launch_bounds__(64 * ScanMap<CPL>::kWaves)
+gdn_prefill_kernel(typename Storage<Tag>::T* __restrict__ pool,
+                   const int* __restrict__ slot_idx,
+                   const float* __restrict__ q, const float* __restrict__ k,
+                   const float* __restrict__ v, Gates gates, float* __restrict__ y,
+                   int H, int G, int heads_per_group, int T) {
+  using LM = ScanMap<CPL>;
+  const int tile_id = blockIdx.x / LM::kParts;
+  const int part = blockIdx.x - tile_id * LM::kParts;
+  const int b = tile_id / H;
+  const int h = tile_id - b * H;
+  __shared__ StageLds st;
+  prefill_tile<Tag, Gates, CPL>(pool, slot_idx, q, k, v, gates, y, H, G, heads_per_group, T, b,
+                                h, part, gates.row_len(b, T), st);
+}
+
+// Ragged batches: the rows' live lengths decide the layout. Every workgroup
+// derives the same plan from seq_lens:
+//   * rows ranked by live length, longest first (ties by row index);
+//   * the rows longer than kSplitFrac of the longest are "long": each of their
+//     tiles is split over two workgroups (one column per lane), which cuts the
+//     serial per-token latency by about a quarter; the rest run whole (two
+//     columns per lane). Splitting pays only if every long row is split, so if
+//     that would need more than max_wgs workgroups, no row is split.
+//   * workgroup order: the long rows' half tiles first, then the other rows'
+//     tiles, longest rows first, so the longest chains start on CUs of their
+//     own and the short rows fill in. Workgroups beyond the plan return.
+// A row's tiles compute the same bits in either layout.
+constexpr float kSplitFrac = 0.8f;
+constexpr int kMaxPlanRows = 1024;
+
+template <class Tag, class Gates>
+__global__ void __launch_bounds__(256)
+gdn_prefill_planned_kernel(typename Storage<Tag>::T* __restrict__ pool,
+                           const int* __restrict__ slot_idx,
+                           const float* __restrict__ q, const float* __restrict__ k,
+                           const float* __restrict__ v, Gates gates, float* __restrict__ y,
+                           int B, int H, int G, int heads_per_group, int T, int max_wgs) {
+  __shared__ StageLds st;
+  __shared__ int lens[kMaxPlanRows];
+  __shared__ int order[kMaxPlanRows];  // row of each rank
+  __shared__ int n_long;
+  for (int r = threadIdx.x; r < B; r += blockDim.x) lens[r] = gates.row_len(r, T);
+  __syncthreads();
+  for (int r = threadIdx.x; r < B; r += blockDim.x) {
+    int rank = 0;
+    for (int o = 0; o < B; ++o)
+      rank += (lens[o] > lens[r] || (lens[o] == lens[r] && o < r)) ? 1 : 0;
+    order[rank] = r;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const float cut = kSplitFrac * (float)lens[order[0]];
+    int s = 0;
+    while (s < B && (float)lens[order[s]] > cut) ++s;
+    n_long = ((B + s) * H <= max_wgs) ? s : 0;
+  }
+  __syncthreads();
+  const int S = n_long;
+  const int i = blockIdx.x;
+  if (i < 2 * S * H) {
+    const int rank = i / (2 * H), rem = i - rank * 2 * H;
+    const int b = order[rank];
+    prefill_tile<Tag, Gates, 1>(pool, slot_idx, q, k, v, gates, y, H, G, heads_per_group, T, b,
+                                rem >> 1, rem & 1, lens[b], st);
+  } else if (i - 2 * S * H < (B - S) * H) {
+    const int w = i - 2 * S * H;
+    const int rank = S + w / H;
+    const int b = order[rank];
+    prefill_tile<Tag, Gates, 2>(pool, slot_idx, q, k, v, gates, y, H, G, heads_per_group, T, b,
+                                w - (w / H) * H, 0, lens[b], st);
   }
 }
 
@@ -446,17 +538,28 @@ int launch_decode(void* pool, int pool_dtype, const int32_t* slot_idx, int B, in
   return st != BRAID_OK ? st : ok();
 }
 
-// Columns per lane of a prefill launch: one (two workgroups per tile, each
-// wave carrying half the per-token work) when that still leaves no CU with a
-// second workgroup, else two. BRAID_PREFILL_COLS (1 or 2) overrides it.
-int prefill_cols(int n_tiles) {
-  const char* env = std::getenv("BRAID_PREFILL_COLS");
-  if (env != nullptr && (std::atoi(env) == 1 || std::atoi(env) == 2)) return std::atoi(env);
+int device_cus() {
   int dev = 0, cus = 0;
   if (hipGetDevice(&dev) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-    return 2;
-  return 2 * n_tiles <= cus ? 1 : 2;
+    return 0;
+  return cus;
+}
+
+// Prefill layout of a launch:
+//   1: one column per lane for every tile (two workgroups per tile), when that
+//      still leaves no CU with a second workgroup;
+//   2: two columns per lane for every tile;
+//   0: planned per row from seq_lens (gdn_prefill_planned_kernel), for larger
+//      ragged batches.
+// BRAID_PREFILL_COLS (1, 2, or 0 for planned when seq_lens is given)
+// overrides the choice.
+int prefill_layout(int n_tiles, int B, bool ragged, int cus) {
+  const char* env = std::getenv("BRAID_PREFILL_COLS");
+  if (env != nullptr && (std::atoi(env) == 1 || std::atoi(env) == 2)) return std::atoi(env);
+  if (env != nullptr && env[0] == '0' && ragged && B <= kMaxPlanRows) return 0;
+  if (cus > 0 && 2 * n_tiles <= cus) return 1;
+  return ragged && B <= kMaxPlanRows && cus > 0 ? 0 : 2;
 }
 
 template <class Gates, int CPL>
@@ -483,15 +586,43 @@ void launch_prefill_cols(void* pool, int pool_dtype, const int32_t* slot_idx, in
 }
 
 template <class Gates>
+void launch_prefill_planned(void* pool, int pool_dtype, const int32_t* slot_idx, int B, int T,
+                            int H, int G, const float* q, const float* k, const float* v,
+                            Gates gates, float* y, int cus, hipStream_t stream) {
+  // Room for every tile plus a split of every row; the plan uses what it needs.
+  const dim3 grid((unsigned)(2 * B * H)), block(256);
+  const int hpg = H / G, max_wgs = cus + cus / 4;
+  switch (pool_dtype) {
+    case BRAID_F32:
+      gdn_prefill_planned_kernel<F32, Gates><<<grid, block, 0, stream>>>(
+          static_cast<float*>(pool), slot_idx, q, k, v, gates, y, B, H, G, hpg, T, max_wgs);
+      break;
+    case BRAID_F16:
+      gdn_prefill_planned_kernel<F16, Gates><<<grid, block, 0, stream>>>(
+          static_cast<uint16_t*>(pool), slot_idx, q, k, v, gates, y, B, H, G, hpg, T, max_wgs);
+      break;
+    default:
+      gdn_prefill_planned_kernel<BF16, Gates><<<grid, block, 0, stream>>>(
+          static_cast<uint16_t*>(pool), slot_idx, q, k, v, gates, y, B, H, G, hpg, T, max_wgs);
+      break;
+  }
+}
+
+template <class Gates>
 int launch_prefill(void* pool, int pool_dtype, const int32_t* slot_idx, int B, int T, int H,
                    int G, const float* q, const float* k, const float* v, Gates gates,
                    float* y, hipStream_t stream) {
-  if (prefill_cols(B * H) == 1)
+  const int cus = device_cus();
+  const int layout = prefill_layout(B * H, B, gates.ragged(), cus);
+  if (layout == 1)
     launch_prefill_cols<Gates, 1>(pool, pool_dtype, slot_idx, B, T, H, G, q, k, v, gates, y,
                                   stream);
-  else
+  else if (layout == 2)
     launch_prefill_cols<Gates, 2>(pool, pool_dtype, slot_idx, B, T, H, G, q, k, v, gates, y,
                                   stream);
+  else
+    launch_prefill_planned<Gates>(pool, pool_dtype, slot_idx, B, T, H, G, q, k, v, gates, y,
+                                  cus > 0 ? cus : 256, stream);
   const int st = hip_status(hipGetLastError(), "launching gdn_prefill_kernel");
   return st != BRAID_OK ? st : ok();
 }

@@ -253,6 +253,10 @@ struct PrecomputedGates {
   }
   __device__ __forceinline__ float eval_alpha(const GateRaw& r, int) const { return r.x0; }
   __device__ __forceinline__ float eval_beta(const GateRaw& r) const { return r.x1; }
+  // Live columns of row b: all T (the caller pads with alpha = 1, beta = 0,
+  // gdn_decode.cu:553-579, which runs them).
+  __device__ __forceinline__ int row_len(int, int T) const { return T; }
+  __host__ __device__ bool ragged() const { return false; }
 };
 
 template <class ActTag>
@@ -297,6 +301,14 @@ struct RawGates {
     const float sp = x > 20.f ? x : log1pf(expf(x));
     return expf(A[h] * sp);
   }
+  // Live columns of row b: seq_lens[b] clamped to [0, T] (a length beyond T
+  // or below 0 is legal, test_gdn_raw_gates.py:234-256), or all T.
+  __device__ __forceinline__ int row_len(int b, int T) const {
+    if (seq_lens == nullptr) return T;
+    const int n = seq_lens[b];
+    return n < 0 ? 0 : (n > T ? T : n);
+  }
+  __host__ __device__ bool ragged() const { return seq_lens != nullptr; }
   __device__ __forceinline__ float eval_beta(const GateRaw& r) const {
     if (r.pad) return 0.f;
     const float e = expf(-r.x1);

@@ -143,6 +143,10 @@ def test_prefill_raw_gates_equal_the_torch_computed_ones(kern, T, act):
 
 
 def test_seq_lens_is_the_where_mask_bit_for_bit(kern):
+    """seq_lens gives the states and the live outputs of the reference's
+    where-mask (gdn.py:313-316) bit for bit. The kernel skips the pad steps
+    (exact identities) and writes 0 at the pad outputs, which the reference
+    leaves unspecified."""
     B, T = 4, 12
     inp = prefill_inputs(B, T, H=32, G=16, seed=41)
     a_raw, b_raw, A, dtb = raw_gates((B, T, 32), 32, torch.bfloat16, seed=43)
@@ -156,7 +160,10 @@ def test_seq_lens_is_the_where_mask_bit_for_bit(kern):
     y1, y2 = torch.empty(B, T, 32, 128, device=DEV), torch.empty(B, T, 32, 128, device=DEV)
     kern.gdn_prefill(p1, slots, inp["q"], inp["k"], inp["v"], am, bm, y1)
     kern.gdn_prefill_raw(p2, slots, inp["q"], inp["k"], inp["v"], a_raw, b_raw, A, dtb, y2, lens)
-    assert torch.equal(p1, p2) and torch.equal(y1, y2)
+    assert torch.equal(p1, p2)
+    lv = live[:, :, 0]
+    assert torch.equal(y1[lv], y2[lv])
+    assert bool((y2[~lv] == 0).all()), "pad outputs must be 0"
 
 
 def test_a_len_of_zero_and_a_len_beyond_t_are_legal(kern):
@@ -170,6 +177,7 @@ def test_a_len_of_zero_and_a_len_beyond_t_are_legal(kern):
     y = torch.empty(B, T, 32, 128, device=DEV)
     kern.gdn_prefill_raw(p, slots, inp["q"], inp["k"], inp["v"], a_raw, b_raw, A, dtb, y, lens)
     assert torch.equal(p[0], before)
+    assert bool((y[0] == 0).all()), "a row of length 0 outputs zeros"
     pr = pool(B, H=32)
     yr = torch.empty_like(y)
     kern.gdn_prefill_raw(pr, slots, inp["q"], inp["k"], inp["v"], a_raw, b_raw, A, dtb, yr, None)
@@ -234,14 +242,15 @@ def test_identity_steps_are_exact_up_to_the_sign_of_zero(kern, dt):
     assert torch.equal(pr, pd) and _same_up_to_zero_sign(pr, pd, dt)
 
 
-@pytest.mark.parametrize("cols", ["1", "2"], ids=["split-1col", "whole-2col"])
+@pytest.mark.parametrize("cols", ["1", "2", "0"], ids=["split-1col", "whole-2col", "planned"])
 @pytest.mark.parametrize("dt", POOL_DTYPES, ids=POOL_IDS)
 def test_both_scan_layouts_are_decode_bit_for_bit(kern, monkeypatch, dt, cols):
     """The launch picks one column per lane (a tile split over two workgroups)
-    for small launches and two otherwise (BRAID_PREFILL_COLS forces either).
-    Both must equal decode applied T times, with raw gates and ragged
-    seq_lens, on every pool type; the automatic choice of one batch size
-    would otherwise leave the other layout untested."""
+    for small launches, two otherwise, or, for larger ragged batches, a plan
+    per row (BRAID_PREFILL_COLS = 1, 2 or 0 forces each; here the planned
+    launch splits the 40-token row and runs the others whole). Every layout
+    must equal decode applied T times, with raw gates and ragged seq_lens
+    including 0, on every pool type, with zeros at the pad outputs."""
     monkeypatch.setenv("BRAID_PREFILL_COLS", cols)
     B, T, H, G = 3, 40, 32, 16
     inp = prefill_inputs(B, T, H=H, G=G, seed=21)
@@ -261,6 +270,9 @@ def test_both_scan_layouts_are_decode_bit_for_bit(kern, monkeypatch, dt, cols):
                             inp["k"][live, t].contiguous(), inp["v"][live, t].contiguous(),
                             a[live, t].contiguous(), b[live, t].contiguous(), A, dtb, yt)
         assert torch.equal(yc[live, t], yt), f"token {t}: outputs differ"
+        dead = (t >= lens).nonzero().flatten()
+        assert bool((yc[dead, t] == 0).all()), f"token {t}: pad outputs are not 0"
+    assert bool((yc[1] == 0).all())
     torch.cuda.synchronize()
     same = (pc == ps) | (pc.isnan() & ps.isnan())
     assert bool(same.all()), f"states differ by {(pc.float() - ps.float()).abs().max().item():.3e}"
