@@ -292,10 +292,23 @@ struct TokenIn {
   float alpha, beta;
 };
 
+// v and the gates are read first: issued behind the 16 row reads, the
+// compiler placed them after the kv chain and waited for them there.
 template <int CPL>
 __device__ __forceinline__ void read_token(const StageLds& st, int j, int r0, int col0,
                                            TokenIn<CPL>& t) {
   typedef float f32x4 __attribute__((ext_vector_type(4)));
+  const float2 ab = *reinterpret_cast<const float2*>(&st.gate[j][0]);
+  t.alpha = ab.x;
+  t.beta = ab.y;
+  if constexpr (CPL == 2) {
+    const float2 v2 = *reinterpret_cast<const float2*>(&st.v[j][col0]);
+    t.v[0] = v2.x;
+    t.v[1] = v2.y;
+  } else {
+    static_assert(CPL == 1, "one or two columns per lane");
+    t.v[0] = st.v[j][col0];
+  }
 #pragma unroll
   for (int r = 0; r < kRowsPerWave; r += 4) {
     const f32x4 k4 = *reinterpret_cast<const f32x4*>(&st.qk[j][1][r0 + r]);
@@ -306,16 +319,6 @@ __device__ __forceinline__ void read_token(const StageLds& st, int j, int r0, in
       t.qh[r + e] = q4[e];
     }
   }
-  if constexpr (CPL == 2) {
-    const float2 v2 = *reinterpret_cast<const float2*>(&st.v[j][col0]);
-    t.v[0] = v2.x;
-    t.v[1] = v2.y;
-  } else {
-    static_assert(CPL == 1, "one or two columns per lane");
-    t.v[0] = st.v[j][col0];
-  }
-  t.alpha = st.gate[j][0];
-  t.beta = st.gate[j][1];
 }
 
 // The live tokens of one tile, with the state resident in registers. Scan
