@@ -29,6 +29,7 @@ oracle on a sample of rows, one thread, scaled to steps/s at B=128.
 
 "paths" (skip with --no-paths) times the other rows of the hot path on their
 BASELINE shapes, each captured in a hipGraph and timed with events:
+  decode_b128_*_pool  the config-1 step on a bf16 and on an fp32 pool
   prefill_config2   gdn_prefill_raw, 8 ragged rows of U[64, 1024] tokens, fp16
                     pool (tokens/s; FP32 flops vs the 157.3 TFLOP/s peak)
   prefill_tick      gdn_prefill_raw, 4 rows x 256 tokens (config 4's chunks)
@@ -353,6 +354,27 @@ def measure_paths(torch, kern):
         return {"rows": Bp, "max_T": T, "tokens": tok, "ms": round(t * 1e3, 3),
                 "tokens_per_s": round(tok / t, 1), "tflops": round(tf, 2),
                 "fp32_frac": round(tf / FP32_PEAK_TFLOPS, 4)}
+
+    # the config-1 step on bf16 and fp32 pools (one 160-slot pool each; an fp32
+    # pool is 320 MiB, past the 256 MB MALL; the bf16 pool's figure is hot)
+    for label, dt, elem in (("decode_b128_bf16_pool", torch.bfloat16, 2),
+                            ("decode_b128_fp32_pool", torch.float32, 4)):
+        dpool = (torch.randn(SLOTS, H, D, D, generator=g, device=dev) * 0.02).to(dt)
+        dslots = torch.randperm(SLOTS, generator=torch.Generator().manual_seed(7))[:B]
+        dslots = dslots.to(torch.int32).to(dev)
+        dq = torch.randn(B, G, D, generator=g, device=dev)
+        dk = torch.randn(B, G, D, generator=g, device=dev)
+        dv = torch.randn(B, H, D, generator=g, device=dev)
+        da = torch.randn(B, H, generator=g, device=dev).to(torch.bfloat16)
+        db = torch.randn(B, H, generator=g, device=dev).to(torch.bfloat16)
+        dy = torch.empty(B, H, D, device=dev)
+        t = graph_time(torch, lambda: kern.gdn_decode_raw(dpool, dslots, dq, dk, dv, da, db, A,
+                                                          dtb, dy), reps=5, inner=20)
+        nbytes = STEP_BYTES + B * H * D * D * 2 * (elem - 2)
+        out[label] = {"us": round(t * 1e6, 2), "steps_per_s": round(1 / t, 1),
+                      "gbs": round(nbytes / t / 1e9, 1),
+                      "hbm_frac": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4)}
+        del dpool
 
     lens = torch.randint(64, 1025, (8,), generator=torch.Generator().manual_seed(2)).tolist()
     out["prefill_config2"] = prefill_case(lens)
