@@ -31,23 +31,23 @@ gdn_decode_kernel(typename Storage<Tag>::T* __restrict__ pool, const int* __rest
   const int b = blockIdx.x / H;
   const int h = blockIdx.x - b * H;
   const int g = h / heads_per_group;
-  const LaneMap<CPL> L(threadIdx.x);
+  const LaneMap<CPL, std::is_same<Tag, F32>::value> L(threadIdx.x);
 
   // The slot comes from device memory, so one captured graph serves any slot
   // assignment (gdn_decode.cu:230-236).
   __shared__ TileLds lds;
   const int slot = slot_idx[b];
-  ST* tile = pool + ((size_t)slot * H + h) * (kSS * kHD) + L.col0;
+  ST* tile = pool + ((size_t)slot * H + h) * (kSS * kHD);
 
   // Issue the whole tile's loads first. (Loads complete in issue order, so the
   // norms and gates below wait for the tile; issuing the small q/k/v/gate loads
   // ahead of it changed nothing measurable: the step is bound by the state.)
   Row<Tag, CPL> S[kRowsPerLane];
 #pragma unroll
-  for (int i = 0; i < kRowsPerLane; ++i) S[i].load_nt(tile + (size_t)L.row(i) * kHD);
+  for (int i = 0; i < kRowsPerLane; ++i) load_row(S[i], L, tile + (size_t)L.row(i) * kHD);
 
   float vv[CPL];
-  loadN<CPL>(v + (size_t)b * v_row + (size_t)h * kHD + L.col0, vv);
+  load_cols(L, v + (size_t)b * v_row + (size_t)h * kHD, vv);
   QK qk;
   normalize_qk(L, q + (size_t)b * q_row + (size_t)g * kSS, k + (size_t)b * k_row + (size_t)g * kSS,
                qk);
@@ -57,9 +57,9 @@ gdn_decode_kernel(typename Storage<Tag>::T* __restrict__ pool, const int* __rest
   gdn_token<Tag, CPL>(L, S, qk, vv, lds, lds.gate, yy);
 
 #pragma unroll
-  for (int i = 0; i < kRowsPerLane; ++i) S[i].store_nt(tile + (size_t)L.row(i) * kHD);
+  for (int i = 0; i < kRowsPerLane; ++i) store_row(S[i], L, tile + (size_t)L.row(i) * kHD);
   // Each column's totals sit in all lanes of its chunk; one lane per chunk writes them.
-  if (L.stores_y()) storeN<CPL>(y + ((size_t)b * H + h) * kHD + L.col0, yy);
+  if (L.stores_y()) store_cols(L, y + ((size_t)b * H + h) * kHD, yy);
 }
 
 // The conv1d decode step fused into the GDN decode step (one launch for the
@@ -94,11 +94,11 @@ __device__ __forceinline__ void conv_decode_body(typename Storage<Tag>::T* __res
   const int g = blockIdx.x - b * G;
   const int t = threadIdx.x / kTileThreads;
   const int h = g * HPG + t;
-  const LaneMap<CPL> L(threadIdx.x % kTileThreads);
+  const LaneMap<CPL, std::is_same<Tag, F32>::value> L(threadIdx.x % kTileThreads);
 
   __shared__ ConvDecodeLds<HPG> lds;
   const int slot = slot_idx[b];
-  ST* tile = pool + ((size_t)slot * H + h) * (kSS * kHD) + L.col0;
+  ST* tile = pool + ((size_t)slot * H + h) * (kSS * kHD);
 
   // The group's conv channels: segment 0 = q (channels g*SS..), 1 = k
   // (G*SS + g*SS..), 2 + j = v of head g*HPG + j (2*G*SS + head*HD..).
@@ -129,7 +129,7 @@ __device__ __forceinline__ void conv_decode_body(typename Storage<Tag>::T* __res
       }
     }
 #pragma unroll
-    for (int i = 0; i < kRowsPerLane; ++i) S[i].load_nt(tile + (size_t)L.row(i) * kHD);
+    for (int i = 0; i < kRowsPerLane; ++i) load_row(S[i], L, tile + (size_t)L.row(i) * kHD);
 #pragma unroll
     for (int m = 0; m < kPer; ++m) {
       const int e = threadIdx.x + m * kThreads;
@@ -141,7 +141,7 @@ __device__ __forceinline__ void conv_decode_body(typename Storage<Tag>::T* __res
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < kRowsPerLane; ++i) S[i].load_nt(tile + (size_t)L.row(i) * kHD);
+    for (int i = 0; i < kRowsPerLane; ++i) load_row(S[i], L, tile + (size_t)L.row(i) * kHD);
     for (int e = threadIdx.x; e < kConv; e += kThreads) {
       const int c = channel(e), seg = e / kHD;
       float* st = conv_pool + ((size_t)slot * C + c) * kK;
@@ -155,15 +155,15 @@ __device__ __forceinline__ void conv_decode_body(typename Storage<Tag>::T* __res
   __syncthreads();
 
   float vv[CPL];
-  loadN<CPL>(&lds.qkv[2 + t][L.col0], vv);
+  load_cols(L, lds.qkv[2 + t], vv);
   QK qk;
   normalize_qk(L, lds.qkv[0], lds.qkv[1], qk);
   publish_gates(L, gates, gates.load(b, h, 0, H, 1), h, lds.tile[t]);
   float yy[CPL];
   gdn_token<Tag, CPL>(L, S, qk, vv, lds.tile[t], lds.tile[t].gate, yy);
 #pragma unroll
-  for (int i = 0; i < kRowsPerLane; ++i) S[i].store_nt(tile + (size_t)L.row(i) * kHD);
-  if (L.stores_y()) storeN<CPL>(y + ((size_t)b * H + h) * kHD + L.col0, yy);
+  for (int i = 0; i < kRowsPerLane; ++i) store_row(S[i], L, tile + (size_t)L.row(i) * kHD);
+  if (L.stores_y()) store_cols(L, y + ((size_t)b * H + h) * kHD, yy);
 }
 
 // Two entry kernels over the same body. A 16-bit pool's body fits in 128

@@ -138,6 +138,27 @@ struct Row<F32, N> {
     d[c] = x0;
     d[c + 1] = x1;
   }
+  // The row's elements as two halves at p0 and p1 (the split column layout).
+  typedef float half_vec __attribute__((ext_vector_type(N / 2)));
+  __device__ __forceinline__ void load_nt_halves(const float* p0, const float* p1) {
+    const half_vec a = __builtin_nontemporal_load(reinterpret_cast<const half_vec*>(p0));
+    const half_vec b = __builtin_nontemporal_load(reinterpret_cast<const half_vec*>(p1));
+#pragma unroll
+    for (int c = 0; c < N / 2; ++c) {
+      d[c] = a[c];
+      d[c + N / 2] = b[c];
+    }
+  }
+  __device__ __forceinline__ void store_nt_halves(float* p0, float* p1) const {
+    half_vec a, b;
+#pragma unroll
+    for (int c = 0; c < N / 2; ++c) {
+      a[c] = d[c];
+      b[c] = d[c + N / 2];
+    }
+    __builtin_nontemporal_store(a, reinterpret_cast<half_vec*>(p0));
+    __builtin_nontemporal_store(b, reinterpret_cast<half_vec*>(p1));
+  }
 };
 
 template <int N>
@@ -317,23 +338,33 @@ struct RawGates {
 };
 
 // ---------------------------------------------------------------------------
-// Lane geometry within a tile when each lane owns CPL columns (8 or 4).
-template <int CPL>
+// Lane geometry within a tile when each lane owns CPL columns.
+//
+// kSplit (fp32 pools): the lane's CPL columns are two runs of CPL / 2, at
+// cc * CPL / 2 and 64 columns further, instead of one run at cc * CPL. A
+// lane's fp32 row chunk is then two 16-byte pieces 256 bytes apart, and every
+// wave-wide load or store of a piece covers four 256-byte half rows, where
+// one run of 32 bytes per lane would leave every other 16 bytes to a second
+// instruction. Sums run over rows within a column, so which lane holds a
+// column changes no bit.
+template <int CPL, bool kSplit = false>
 struct LaneMap {
   static constexpr int kGroupCols = kLanesPerRowGroup * CPL;  // columns per wave group
+  static constexpr bool kSplitCols = kSplit;
+  static constexpr int kRun = kSplit ? CPL / 2 : CPL;         // contiguous columns per run
   int wave;  // 0..(waves per tile - 1)
   int w;     // row block 0..3: rows [32 w, 32 w + 32)
   int lane;  // 0..63
   int rg;    // row group 0..3
   int cc;    // column chunk within the wave's column group, 0..15
-  int col0;  // first of this lane's CPL columns
+  int col0;  // first of this lane's columns
   __device__ __forceinline__ LaneMap(int tid) {
     lane = tid & 63;
     wave = tid >> 6;
     w = wave % kWaves;
     rg = lane / kLanesPerRowGroup;
     cc = lane % kLanesPerRowGroup;
-    col0 = (wave / kWaves) * kGroupCols + cc * CPL;
+    col0 = (wave / kWaves) * kGroupCols + cc * kRun;
   }
   __device__ __forceinline__ int row(int i) const {
     return w * kRowsPerWave + rg + kRowGroups * i;
@@ -342,6 +373,52 @@ struct LaneMap {
   // cc / 4 (the four row blocks share the stores).
   __device__ __forceinline__ bool stores_y() const { return rg == 0 && cc / 4 == w; }
 };
+
+// The lane's CPL values of a [kHD] vector (v, y, an LDS exchange row) in its
+// column order: one run, or two runs 64 columns apart.
+template <int CPL, bool S>
+__device__ __forceinline__ void load_cols(const LaneMap<CPL, S>& L, const float* base,
+                                          float (&out)[CPL]) {
+  typedef float vec __attribute__((ext_vector_type(LaneMap<CPL, S>::kRun)));
+  constexpr int R = LaneMap<CPL, S>::kRun;
+#pragma unroll
+  for (int run = 0; run < CPL / R; ++run) {
+    const vec a = *reinterpret_cast<const vec*>(base + L.col0 + run * (kHD / 2));
+#pragma unroll
+    for (int c = 0; c < R; ++c) out[run * R + c] = a[c];
+  }
+}
+template <int CPL, bool S>
+__device__ __forceinline__ void store_cols(const LaneMap<CPL, S>& L, float* base,
+                                           const float (&in)[CPL]) {
+  typedef float vec __attribute__((ext_vector_type(LaneMap<CPL, S>::kRun)));
+  constexpr int R = LaneMap<CPL, S>::kRun;
+#pragma unroll
+  for (int run = 0; run < CPL / R; ++run) {
+    vec a;
+#pragma unroll
+    for (int c = 0; c < R; ++c) a[c] = in[run * R + c];
+    *reinterpret_cast<vec*>(base + L.col0 + run * (kHD / 2)) = a;
+  }
+}
+
+// A state row's CPL elements of this lane, from / to the row starting at `row`.
+template <class Tag, int CPL, bool S>
+__device__ __forceinline__ void load_row(Row<Tag, CPL>& r, const LaneMap<CPL, S>& L,
+                                         const typename Storage<Tag>::T* row) {
+  if constexpr (S)
+    r.load_nt_halves(row + L.col0, row + L.col0 + kHD / 2);
+  else
+    r.load_nt(row + L.col0);
+}
+template <class Tag, int CPL, bool S>
+__device__ __forceinline__ void store_row(const Row<Tag, CPL>& r, const LaneMap<CPL, S>& L,
+                                          typename Storage<Tag>::T* row) {
+  if constexpr (S)
+    r.store_nt_halves(row + L.col0, row + L.col0 + kHD / 2);
+  else
+    r.store_nt(row + L.col0);
+}
 
 // Lane geometry of the scan (prefill) layout: a lane holds all 32 rows of its
 // row block w for CPL columns, so the row-group level of every column sum is
@@ -471,27 +548,20 @@ __device__ __forceinline__ void normalize_qk(const LM& L, const float* __restric
 //   column_sums_take:  after the barrier, read the four row blocks' partials
 //                      and add them by the fixed tree (w0 + w1) + (w2 + w3).
 // Every lane ends with the totals of its columns.
-template <int CPL>
-__device__ __forceinline__ void column_sums_post(const LaneMap<CPL>& L, float (&part)[CPL],
+template <int CPL, bool S>
+__device__ __forceinline__ void column_sums_post(const LaneMap<CPL, S>& L, float (&part)[CPL],
                                                  float (*buf)[kHD]) {
-  typedef float vec __attribute__((ext_vector_type(CPL)));
 #pragma unroll
   for (int c = 0; c < CPL; ++c) part[c] = rowgroup_sum(part[c]);
-  if (L.rg == 0) {
-    vec p;
-#pragma unroll
-    for (int c = 0; c < CPL; ++c) p[c] = part[c];
-    *reinterpret_cast<vec*>(&buf[L.w][L.col0]) = p;
-  }
+  if (L.rg == 0) store_cols(L, buf[L.w], part);
 }
 
-template <int CPL>
-__device__ __forceinline__ void column_sums_take(const LaneMap<CPL>& L, float (&part)[CPL],
+template <int CPL, bool S>
+__device__ __forceinline__ void column_sums_take(const LaneMap<CPL, S>& L, float (&part)[CPL],
                                                  float (*buf)[kHD]) {
-  typedef float vec __attribute__((ext_vector_type(CPL)));
-  vec wv[kWaves];
+  float wv[kWaves][CPL];
 #pragma unroll
-  for (int j = 0; j < kWaves; ++j) wv[j] = *reinterpret_cast<const vec*>(&buf[j][L.col0]);
+  for (int j = 0; j < kWaves; ++j) load_cols(L, buf[j], wv[j]);
 #pragma unroll
   for (int c = 0; c < CPL; ++c) part[c] = (wv[0][c] + wv[1][c]) + (wv[2][c] + wv[3][c]);
 }
@@ -543,21 +613,21 @@ __device__ __forceinline__ void update_state(Row<Tag, CPL> (&S)[kRowsPerLane], c
 // `gate` ([alpha, beta]) after the first barrier, so whoever writes them must
 // do so before it (publish_gates). Contains two workgroup barriers, so all
 // waves of the tile must call it together.
-template <class Tag, int CPL>
-__device__ __forceinline__ void gdn_token(const LaneMap<CPL>& L,
+template <class Tag, int CPL, bool kSplit>
+__device__ __forceinline__ void gdn_token(const LaneMap<CPL, kSplit>& L,
                                           Row<Tag, CPL> (&S)[kRowsPerLane], const QK& qk,
                                           const float (&v)[CPL], TileLds& lds,
                                           const float* gate, float (&y)[CPL]) {
   float kv[CPL];
   kv_partials<Tag, CPL>(S, qk, kv);
-  column_sums_post<CPL>(L, kv, lds.kv);
+  column_sums_post(L, kv, lds.kv);
   __syncthreads();
-  column_sums_take<CPL>(L, kv, lds.kv);
+  column_sums_take(L, kv, lds.kv);
   float acc[CPL];
   update_state<Tag, CPL>(S, qk, v, kv, gate[0], gate[1], acc);
-  column_sums_post<CPL>(L, acc, lds.y);
+  column_sums_post(L, acc, lds.y);
   __syncthreads();
-  column_sums_take<CPL>(L, acc, lds.y);
+  column_sums_take(L, acc, lds.y);
 #pragma unroll
   for (int c = 0; c < CPL; ++c) y[c] = acc[c] * kYScale;
 }
