@@ -376,6 +376,19 @@ def measure_paths(torch, kern):
                       "hbm_frac": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4)}
         del dpool
 
+    # gdn_decode (gates precomputed in fp32) on the config-1 fp16 pool shape:
+    # alpha and beta are 8 bytes per head instead of the raw gates' 4
+    dpool = (torch.randn(SLOTS, H, D, D, generator=g, device=dev) * 0.02).half()
+    dalpha = torch.rand(B, H, generator=g, device=dev) * 0.5 + 0.5
+    dbeta = torch.rand(B, H, generator=g, device=dev)
+    t = graph_time(torch, lambda: kern.gdn_decode(dpool, dslots, dq, dk, dv, dalpha, dbeta, dy),
+                   reps=5, inner=20)
+    nbytes = STEP_BYTES + B * H * 4
+    out["decode_b128_fp16_precomputed_gates"] = {
+        "us": round(t * 1e6, 2), "steps_per_s": round(1 / t, 1),
+        "gbs": round(nbytes / t / 1e9, 1), "hbm_frac": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4)}
+    del dpool
+
     lens = torch.randint(64, 1025, (8,), generator=torch.Generator().manual_seed(2)).tolist()
     out["prefill_config2"] = prefill_case(lens)
 

@@ -39,19 +39,33 @@ gdn_decode_kernel(typename Storage<Tag>::T* __restrict__ pool, const int* __rest
   const int slot = slot_idx[b];
   ST* tile = pool + ((size_t)slot * H + h) * (kSS * kHD);
 
-  // Issue the whole tile's loads first. (Loads complete in issue order, so the
-  // norms and gates below wait for the tile; issuing the small q/k/v/gate loads
-  // ahead of it changed nothing measurable: the step is bound by the state.)
+  // The gates come through the scalar unit (load_uniform), so their arithmetic
+  // runs while the tile is still in flight. The q/k/v loads go ahead of the
+  // tile too for 16-bit pools (loads complete in issue order, so the norms then
+  // wait only for them); an fp32 pool's body has no registers to spare for
+  // that and issues them after the tile.
+  constexpr bool kEarly = !std::is_same<Tag, F32>::value;
+  const GateRaw gr = gates.load_uniform(b, h, H);
+  const float* qg = q + (size_t)b * q_row + (size_t)g * kSS;
+  const float* kg = k + (size_t)b * k_row + (size_t)g * kSS;
+  const float* vh = v + (size_t)b * v_row + (size_t)h * kHD;
+  QKRaw qkr;
+  float vv[CPL];
+  if (kEarly) {
+    load_qk(L, qg, kg, qkr);
+    load_cols(L, vh, vv);
+  }
   Row<Tag, CPL> S[kRowsPerLane];
 #pragma unroll
   for (int i = 0; i < kRowsPerLane; ++i) load_row(S[i], L, tile + (size_t)L.row(i) * kHD);
+  if (!kEarly) {
+    load_cols(L, vh, vv);
+    load_qk(L, qg, kg, qkr);
+  }
 
-  float vv[CPL];
-  load_cols(L, v + (size_t)b * v_row + (size_t)h * kHD, vv);
+  publish_gates(L, gates, gr, h, lds);
   QK qk;
-  normalize_qk(L, q + (size_t)b * q_row + (size_t)g * kSS, k + (size_t)b * k_row + (size_t)g * kSS,
-               qk);
-  publish_gates(L, gates, gates.load(b, h, 0, H, 1), h, lds);
+  normalize_qk(qkr, qk);
 
   float yy[CPL];
   gdn_token<Tag, CPL>(L, S, qk, vv, lds, lds.gate, yy);
@@ -517,6 +531,20 @@ int check_act(const void* a_raw, const void* b_raw, int act_dtype, const float* 
   return BRAID_OK;
 }
 
+// Dynamic LDS requested only to cap resident decode workgroups per CU
+// (BRAID_DECODE_WGS_PER_CU; 0 or unset: no cap).
+size_t decode_lds_pad() {
+  static const size_t pad = [] {
+    const char* e = getenv("BRAID_DECODE_WGS_PER_CU");
+    const int n = e ? atoi(e) : 0;
+    if (n <= 0) return (size_t)0;
+    long p = 163840L / n - (long)sizeof(TileLds) - 1024;
+    if (p > 65536) p = 65536;
+    return p > 0 ? (size_t)p : (size_t)0;
+  }();
+  return pad;
+}
+
 template <class Gates>
 int launch_decode(void* pool, int pool_dtype, const int32_t* slot_idx, int B, int H, int G,
                   const float* q, int64_t q_row, const float* k, int64_t k_row, const float* v,
@@ -525,15 +553,15 @@ int launch_decode(void* pool, int pool_dtype, const int32_t* slot_idx, int B, in
   const int hpg = H / G;
   switch (pool_dtype) {
     case BRAID_F32:
-      gdn_decode_kernel<F32, Gates><<<grid, block, 0, stream>>>(
+      gdn_decode_kernel<F32, Gates><<<grid, block, decode_lds_pad(), stream>>>(
           static_cast<float*>(pool), slot_idx, q, k, v, gates, y, H, hpg, q_row, k_row, v_row);
       break;
     case BRAID_F16:
-      gdn_decode_kernel<F16, Gates><<<grid, block, 0, stream>>>(
+      gdn_decode_kernel<F16, Gates><<<grid, block, decode_lds_pad(), stream>>>(
           static_cast<uint16_t*>(pool), slot_idx, q, k, v, gates, y, H, hpg, q_row, k_row, v_row);
       break;
     default:
-      gdn_decode_kernel<BF16, Gates><<<grid, block, 0, stream>>>(
+      gdn_decode_kernel<BF16, Gates><<<grid, block, decode_lds_pad(), stream>>>(
           static_cast<uint16_t*>(pool), slot_idx, q, k, v, gates, y, H, hpg, q_row, k_row, v_row);
       break;
   }

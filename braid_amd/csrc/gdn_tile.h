@@ -264,6 +264,25 @@ struct GateRaw {
   bool pad;      // a pad column: alpha = 1, beta = 0
 };
 
+// Loads of one value at a wave-uniform address through the scalar unit
+// (s_load): read through the constant address space, which the kernels never
+// write. A scalar load is counted apart from the vector memory queue, so
+// reading a value this way does not wait behind the state tile's loads. A
+// 16-bit value is taken out of its aligned dword (an aligned 4-byte read
+// cannot cross a page, so it cannot fault past the end of the tensor).
+typedef const __attribute__((address_space(4))) uint32_t* const_u32_ptr;
+__device__ __forceinline__ float load_uniform(const float* p) {
+  return __uint_as_float(*reinterpret_cast<const_u32_ptr>(reinterpret_cast<uintptr_t>(p)));
+}
+__device__ __forceinline__ uint32_t load_uniform(const uint16_t* p) {
+  const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+  const uint32_t w = *reinterpret_cast<const_u32_ptr>(a & ~(uintptr_t)3);
+  return (w >> ((a & 2) * 8)) & 0xffffu;
+}
+__device__ __forceinline__ int load_uniform(const int* p) {
+  return (int)*reinterpret_cast<const_u32_ptr>(reinterpret_cast<uintptr_t>(p));
+}
+
 // Gates the caller computed (gdn_decode.cu:102-110): [B, T, H] fp32.
 struct PrecomputedGates {
   const float* alpha;
@@ -271,6 +290,11 @@ struct PrecomputedGates {
   __device__ __forceinline__ GateRaw load(int b, int h, int t, int H, int T) const {
     const size_t i = ((size_t)b * T + t) * H + h;
     return GateRaw{alpha[i], beta[i], false};
+  }
+  // One decode token's gates (T = 1), at a wave-uniform index.
+  __device__ __forceinline__ GateRaw load_uniform(int b, int h, int H) const {
+    const size_t i = (size_t)b * H + h;
+    return GateRaw{braid::load_uniform(alpha + i), braid::load_uniform(beta + i), false};
   }
   __device__ __forceinline__ float eval_alpha(const GateRaw& r, int) const { return r.x0; }
   __device__ __forceinline__ float eval_beta(const GateRaw& r) const { return r.x1; }
@@ -315,6 +339,12 @@ struct RawGates {
     if (seq_lens != nullptr && t >= seq_lens[b]) return GateRaw{0.f, 0.f, true};
     const size_t i = ((size_t)b * T + t) * H + h;
     return GateRaw{ActRead<ActTag>::widen(a_raw[i]), ActRead<ActTag>::widen(b_raw[i]), false};
+  }
+  __device__ __forceinline__ GateRaw load_uniform(int b, int h, int H) const {
+    const size_t i = (size_t)b * H + h;
+    const bool pad = seq_lens != nullptr && braid::load_uniform(seq_lens + b) <= 0;
+    return GateRaw{ActRead<ActTag>::widen(braid::load_uniform(a_raw + i)),
+                   ActRead<ActTag>::widen(braid::load_uniform(b_raw + i)), pad};
   }
   __device__ __forceinline__ float eval_alpha(const GateRaw& r, int h) const {
     if (r.pad) return 1.f;

@@ -72,3 +72,23 @@ def test_decode_state_uses_128_bit_nontemporal_accesses(asm):
     text = asm["gdn_scan.hip"]
     assert re.search(r"global_load_dwordx4 .* nt", text)
     assert re.search(r"global_store_dwordx4 .* nt", text)
+
+
+def test_decode_kernels_fit_four_waves_per_simd(asm):
+    """The decode kernels are bound by the state stream, which needs four
+    resident workgroups per CU (four waves per SIMD) to keep enough bytes in
+    flight; that holds only at <= 128 architectural VGPRs per lane. Every
+    instantiation (each pool dtype and gate policy, fused conv or not) is
+    checked: the compiler's register count moves with small changes to the
+    body's order."""
+    text = asm["gdn_scan.hip"]
+    found = []
+    for m in re.finditer(r"\.amdhsa_kernel (\S+)(.*?)\.end_amdhsa_kernel", text, re.S):
+        name, body = m.group(1), m.group(2)
+        if "gdn_decode_kernel" not in name and "gdn_conv_decode_kernel" not in name:
+            continue
+        vgpr = int(re.search(r"\.amdhsa_next_free_vgpr\s+(\d+)", body).group(1))
+        found.append((name, vgpr))
+    assert len(found) >= 9 + 24, len(found)
+    over = [(n, v) for n, v in found if v > 128]
+    assert not over, over
