@@ -9,6 +9,7 @@
 // it back; prefill loads it once, runs T tokens with the tile resident in
 // registers (in the pool's storage type) and stores it once. Reference behaviour: braid/kernels/csrc/gdn_decode.cu:156-272 (decode)
 // and :467-551 (prefill); entry-point contracts :313-441 and :553-699.
+#include <atomic>
 #include <cstdlib>
 #include <type_traits>
 
@@ -531,18 +532,48 @@ int check_act(const void* a_raw, const void* b_raw, int act_dtype, const float* 
   return BRAID_OK;
 }
 
-// Dynamic LDS requested only to cap resident decode workgroups per CU
-// (BRAID_DECODE_WGS_PER_CU; 0 or unset: no cap).
-size_t decode_lds_pad() {
-  static const size_t pad = [] {
+// CUs of the current device (0 if the runtime cannot say), cached per device:
+// the decode launch consults it every step.
+int device_cus() {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> cached[kMaxDevices];
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  if (dev >= 0 && dev < kMaxDevices && (cus = cached[dev].load(std::memory_order_relaxed)) > 0)
+    return cus;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return 0;
+  if (dev >= 0 && dev < kMaxDevices) cached[dev].store(cus, std::memory_order_relaxed);
+  return cus;
+}
+
+// Resident decode workgroups per CU, capped by requesting dynamic LDS the
+// kernel does not use. Measured on cold pools (MI355X, 256 CUs, fp16 state):
+// with enough tiles for four or more rounds at three per CU, three resident
+// workgroups stream the state 1.5-3% faster than four (B=128: 51.7 -> 50.4 us;
+// B=256: 101.7 -> 99.7 us); below that the coarser last round costs more
+// (B=32: 14.9 -> 16.0 us). fp32 pools gain nothing from the cap. The
+// BRAID_DECODE_WGS_PER_CU environment variable overrides the choice: N > 0
+// caps at N, 0 leaves it uncapped.
+int decode_wgs_override() {
+  static const int n = [] {
     const char* e = getenv("BRAID_DECODE_WGS_PER_CU");
-    const int n = e ? atoi(e) : 0;
-    if (n <= 0) return (size_t)0;
-    long p = 163840L / n - (long)sizeof(TileLds) - 1024;
-    if (p > 65536) p = 65536;
-    return p > 0 ? (size_t)p : (size_t)0;
+    return e ? atoi(e) : -1;
   }();
-  return pad;
+  return n;
+}
+
+size_t decode_lds_pad(int pool_dtype, long n_tiles) {
+  int cap = decode_wgs_override();
+  if (cap < 0) {
+    const int cus = device_cus();
+    cap = (pool_dtype != BRAID_F32 && cus > 0 && n_tiles >= 12L * cus) ? 3 : 0;
+  }
+  if (cap <= 0) return 0;
+  constexpr long kLdsPerCu = 160 * 1024;
+  long pad = kLdsPerCu / cap - (long)sizeof(TileLds) - 1024;
+  if (pad > 65536) pad = 65536;
+  return pad > 0 ? (size_t)pad : 0;
 }
 
 template <class Gates>
@@ -551,30 +582,23 @@ int launch_decode(void* pool, int pool_dtype, const int32_t* slot_idx, int B, in
                   int64_t v_row, Gates gates, float* y, hipStream_t stream) {
   const dim3 grid((unsigned)B * (unsigned)H), block(tile_threads(kDecodeCols));
   const int hpg = H / G;
+  const size_t lds_pad = decode_lds_pad(pool_dtype, (long)B * H);
   switch (pool_dtype) {
     case BRAID_F32:
-      gdn_decode_kernel<F32, Gates><<<grid, block, decode_lds_pad(), stream>>>(
+      gdn_decode_kernel<F32, Gates><<<grid, block, lds_pad, stream>>>(
           static_cast<float*>(pool), slot_idx, q, k, v, gates, y, H, hpg, q_row, k_row, v_row);
       break;
     case BRAID_F16:
-      gdn_decode_kernel<F16, Gates><<<grid, block, decode_lds_pad(), stream>>>(
+      gdn_decode_kernel<F16, Gates><<<grid, block, lds_pad, stream>>>(
           static_cast<uint16_t*>(pool), slot_idx, q, k, v, gates, y, H, hpg, q_row, k_row, v_row);
       break;
     default:
-      gdn_decode_kernel<BF16, Gates><<<grid, block, decode_lds_pad(), stream>>>(
+      gdn_decode_kernel<BF16, Gates><<<grid, block, lds_pad, stream>>>(
           static_cast<uint16_t*>(pool), slot_idx, q, k, v, gates, y, H, hpg, q_row, k_row, v_row);
       break;
   }
   const int st = hip_status(hipGetLastError(), "launching gdn_decode_kernel");
   return st != BRAID_OK ? st : ok();
-}
-
-int device_cus() {
-  int dev = 0, cus = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-    return 0;
-  return cus;
 }
 
 // Prefill layout of a launch:
