@@ -16,6 +16,7 @@
 #include "capi_common.h"
 #include "conv_common.h"
 #include "gdn_tile.h"
+#include "stream_shape.h"
 
 namespace braid {
 namespace {
@@ -26,11 +27,12 @@ __global__ void __launch_bounds__(tile_threads(kDecodeCols))
 gdn_decode_kernel(typename Storage<Tag>::T* __restrict__ pool, const int* __restrict__ slot_idx,
                   const float* __restrict__ q, const float* __restrict__ k,
                   const float* __restrict__ v, Gates gates, float* __restrict__ y, int H,
-                  int heads_per_group, long q_row, long k_row, long v_row) {
+                  int heads_per_group, long q_row, long k_row, long v_row, int xcd_contiguous) {
   constexpr int CPL = kDecodeCols;
   using ST = typename Storage<Tag>::T;
-  const int b = blockIdx.x / H;
-  const int h = blockIdx.x - b * H;
+  const int tix = stream_tile(xcd_contiguous);
+  const int b = tix / H;
+  const int h = tix - b * H;
   const int g = h / heads_per_group;
   const LaneMap<CPL, std::is_same<Tag, F32>::value> L(threadIdx.x);
 
@@ -547,54 +549,28 @@ int device_cus() {
   return cus;
 }
 
-// Resident decode workgroups per CU, capped by requesting dynamic LDS the
-// kernel does not use. Measured on cold pools (MI355X, 256 CUs, fp16 state):
-// with enough tiles for four or more rounds at three per CU, three resident
-// workgroups stream the state 1.5-3% faster than four (B=128: 51.7 -> 50.4 us;
-// B=256: 101.7 -> 99.7 us); below that the coarser last round costs more
-// (B=32: 14.9 -> 16.0 us). fp32 pools gain nothing from the cap. The
-// BRAID_DECODE_WGS_PER_CU environment variable overrides the choice: N > 0
-// caps at N, 0 leaves it uncapped.
-int decode_wgs_override() {
-  static const int n = [] {
-    const char* e = getenv("BRAID_DECODE_WGS_PER_CU");
-    return e ? atoi(e) : -1;
-  }();
-  return n;
-}
-
-size_t decode_lds_pad(int pool_dtype, long n_tiles) {
-  int cap = decode_wgs_override();
-  if (cap < 0) {
-    const int cus = device_cus();
-    cap = (pool_dtype != BRAID_F32 && cus > 0 && n_tiles >= 12L * cus) ? 3 : 0;
-  }
-  if (cap <= 0) return 0;
-  constexpr long kLdsPerCu = 160 * 1024;
-  long pad = kLdsPerCu / cap - (long)sizeof(TileLds) - 1024;
-  if (pad > 65536) pad = 65536;
-  return pad > 0 ? (size_t)pad : 0;
-}
-
 template <class Gates>
 int launch_decode(void* pool, int pool_dtype, const int32_t* slot_idx, int B, int H, int G,
                   const float* q, int64_t q_row, const float* k, int64_t k_row, const float* v,
                   int64_t v_row, Gates gates, float* y, hipStream_t stream) {
   const dim3 grid((unsigned)B * (unsigned)H), block(tile_threads(kDecodeCols));
   const int hpg = H / G;
-  const size_t lds_pad = decode_lds_pad(pool_dtype, (long)B * H);
+  const StreamShape shape =
+      stream_shape((long)B * H, device_cus(), pool_dtype != BRAID_F32, sizeof(TileLds));
+  const size_t lds_pad = shape.lds_pad;
+  const int xr = shape.xcd_contiguous;
   switch (pool_dtype) {
     case BRAID_F32:
       gdn_decode_kernel<F32, Gates><<<grid, block, lds_pad, stream>>>(
-          static_cast<float*>(pool), slot_idx, q, k, v, gates, y, H, hpg, q_row, k_row, v_row);
+          static_cast<float*>(pool), slot_idx, q, k, v, gates, y, H, hpg, q_row, k_row, v_row, xr);
       break;
     case BRAID_F16:
       gdn_decode_kernel<F16, Gates><<<grid, block, lds_pad, stream>>>(
-          static_cast<uint16_t*>(pool), slot_idx, q, k, v, gates, y, H, hpg, q_row, k_row, v_row);
+          static_cast<uint16_t*>(pool), slot_idx, q, k, v, gates, y, H, hpg, q_row, k_row, v_row, xr);
       break;
     default:
       gdn_decode_kernel<BF16, Gates><<<grid, block, lds_pad, stream>>>(
-          static_cast<uint16_t*>(pool), slot_idx, q, k, v, gates, y, H, hpg, q_row, k_row, v_row);
+          static_cast<uint16_t*>(pool), slot_idx, q, k, v, gates, y, H, hpg, q_row, k_row, v_row, xr);
       break;
   }
   const int st = hip_status(hipGetLastError(), "launching gdn_decode_kernel");

@@ -5,11 +5,14 @@
 // what an in-place stream of 32 KiB state tiles can reach. Each kernel moves
 // exactly the decode's state bytes with the decode's lane layout (one
 // 256-thread workgroup per tile; lane l of wave w owns the 16-byte chunk l % 16
-// of rows 32 w + l / 16 + 4 i, i = 0..7; nontemporal 128-bit accesses) and
-// nothing else, so decode time / probe time is the share of that ceiling
+// of rows 32 w + l / 16 + 4 i, i = 0..7; nontemporal 128-bit accesses), in
+// the decode's launch shape (stream_shape.h: tile order and resident
+// workgroups per CU), and nothing else, so decode time / probe time is the share of that ceiling
 // the decode reaches with its arithmetic, q/k/v/y traffic and gates included.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include "stream_shape.h"
 
 namespace {
 
@@ -23,8 +26,9 @@ __device__ __forceinline__ int chunk_offset(int i) {
 
 // Read every chunk of the tile and write it back changed (the decode's
 // in-place update of a state tile, without the arithmetic).
-__global__ void __launch_bounds__(256) probe_rmw(char* base, const int* __restrict__ tile_idx) {
-  char* t = base + (size_t)tile_idx[blockIdx.x] * kTileBytes;
+__global__ void __launch_bounds__(256)
+probe_rmw(char* base, const int* __restrict__ tile_idx, int xc) {
+  char* t = base + (size_t)tile_idx[braid::stream_tile(xc)] * kTileBytes;
   u32x4 s[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i)
@@ -37,8 +41,8 @@ __global__ void __launch_bounds__(256) probe_rmw(char* base, const int* __restri
 // Read every chunk; `sink` is written only if the data hits an impossible
 // pattern, which keeps the loads live without adding traffic.
 __global__ void __launch_bounds__(256) probe_read(const char* base, const int* __restrict__ tile_idx,
-                                                  u32x4* sink) {
-  const char* t = base + (size_t)tile_idx[blockIdx.x] * kTileBytes;
+                                                  u32x4* sink, int xc) {
+  const char* t = base + (size_t)tile_idx[braid::stream_tile(xc)] * kTileBytes;
   u32x4 s[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i)
@@ -50,8 +54,9 @@ __global__ void __launch_bounds__(256) probe_read(const char* base, const int* _
 }
 
 // Write every chunk.
-__global__ void __launch_bounds__(256) probe_write(char* base, const int* __restrict__ tile_idx) {
-  char* t = base + (size_t)tile_idx[blockIdx.x] * kTileBytes;
+__global__ void __launch_bounds__(256)
+probe_write(char* base, const int* __restrict__ tile_idx, int xc) {
+  char* t = base + (size_t)tile_idx[braid::stream_tile(xc)] * kTileBytes;
   const u32x4 v = {threadIdx.x, blockIdx.x, 0x3c003c00u, 0x3c003c00u};
 #pragma unroll
   for (int i = 0; i < 8; ++i)
@@ -72,13 +77,22 @@ int braid_probe_stream(int kind, void* base, int64_t n_tiles, const int32_t* til
     return (int)hipErrorInvalidValue;
   const dim3 grid((unsigned)n_tiles), block(256);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  // The decode's launch shape for the same tile count (the decode's 16-bit
+  // tiles hold its exchange buffer, 4,104 bytes of static LDS).
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    cus = 0;
+  const braid::StreamShape sh = braid::stream_shape(n_tiles, cus, true, 4104);
   if (kind == 0)
-    probe_rmw<<<grid, block, 0, s>>>(static_cast<char*>(base), tile_idx);
+    probe_rmw<<<grid, block, sh.lds_pad, s>>>(static_cast<char*>(base), tile_idx,
+                                              sh.xcd_contiguous);
   else if (kind == 1)
-    probe_read<<<grid, block, 0, s>>>(static_cast<const char*>(base), tile_idx,
-                                      static_cast<u32x4*>(sink));
+    probe_read<<<grid, block, sh.lds_pad, s>>>(static_cast<const char*>(base), tile_idx,
+                                               static_cast<u32x4*>(sink), sh.xcd_contiguous);
   else
-    probe_write<<<grid, block, 0, s>>>(static_cast<char*>(base), tile_idx);
+    probe_write<<<grid, block, sh.lds_pad, s>>>(static_cast<char*>(base), tile_idx,
+                                                sh.xcd_contiguous);
   return (int)hipGetLastError();
 }
 

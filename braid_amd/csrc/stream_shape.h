@@ -1,0 +1,69 @@
+// Launch shape of a state stream over 32 KiB tiles (one 256-thread workgroup
+// per tile): the decode kernels and the HBM probe that measures their ceiling
+// share it, so the probe keeps streaming exactly what the decode streams.
+//
+// Two measured choices (MI355X: 256 CUs in 8 XCDs, cold slot-permuted pools),
+// both taken only for a launch of at least 12 tiles per CU ("large"):
+//
+// * XCD-contiguous tiles. The dispatcher deals consecutive workgroups to the
+//   8 XCDs in turn, so tile order t = blockIdx.x hands each XCD every eighth
+//   tile. Remapping workgroup i to tile (i % 8) * (n / 8) + i / 8 gives XCD x
+//   the contiguous range [x n / 8, (x + 1) n / 8) instead, walked in order.
+//   fp16 decode at B = 96/128/192/256 (with the cap below): 39.4 -> 38.3,
+//   51.6 -> 49.4, 75.6 -> 72.6, 100.0 -> 93.8 us; fp32 pool at B = 128:
+//   96.9 -> 95.1 us. Up to B = 64 it changes nothing measurable (B = 8 is 2%
+//   slower), hence the threshold. Needs n % 8 == 0.
+// * Three resident workgroups per CU for 16-bit tiles, not four, by asking for
+//   dynamic LDS the kernel does not use: B = 128 51.7 -> 50.4 us on its own;
+//   with fewer rounds the coarser last round costs more (B = 32: 14.9 ->
+//   16.0 us uncapped vs capped), and fp32 tiles gain nothing.
+//
+// BRAID_DECODE_XCD_REMAP (0 / 1) and BRAID_DECODE_WGS_PER_CU (0: uncapped,
+// N > 0: N) override the choices, for measurement.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdlib.h>
+
+namespace braid {
+
+constexpr int kXcds = 8;
+
+// The tile a workgroup streams (see above).
+__device__ __forceinline__ int stream_tile(int xcd_contiguous) {
+  if (!xcd_contiguous) return blockIdx.x;
+  const int per = gridDim.x / kXcds;
+  return (blockIdx.x % kXcds) * per + blockIdx.x / kXcds;
+}
+
+struct StreamShape {
+  int xcd_contiguous;  // argument of stream_tile
+  size_t lds_pad;      // dynamic LDS bytes to request
+};
+
+inline int env_override(const char* name) {
+  const char* e = getenv(name);
+  return e ? atoi(e) : -1;
+}
+
+// cus: CUs of the device (0 if unknown: no large-launch choices);
+// narrow: 16-bit tiles; static_lds: the kernel's own LDS bytes.
+inline StreamShape stream_shape(long n_tiles, int cus, bool narrow, size_t static_lds) {
+  static const int remap_env = env_override("BRAID_DECODE_XCD_REMAP");
+  static const int cap_env = env_override("BRAID_DECODE_WGS_PER_CU");
+  const bool large = cus > 0 && n_tiles >= 12L * cus;
+  StreamShape s{0, 0};
+  const bool remap = remap_env >= 0 ? remap_env > 0 : large;
+  s.xcd_contiguous = (remap && n_tiles % kXcds == 0) ? 1 : 0;
+  const int cap = cap_env >= 0 ? cap_env : (large && narrow ? 3 : 0);
+  if (cap > 0) {
+    constexpr long kLdsPerCu = 160 * 1024;
+    long pad = kLdsPerCu / cap - (long)static_lds - 1024;
+    if (pad > 65536) pad = 65536;
+    s.lds_pad = pad > 0 ? (size_t)pad : 0;
+  }
+  return s;
+}
+
+}  // namespace braid
