@@ -353,7 +353,7 @@ __device__ __forceinline__ void read_token(const StageLds& st, int j, int r0, in
 // into +0. y at the pad positions [len, T) is written as 0 (the reference
 // leaves arbitrary values there that nothing reads; zeros also keep a later
 // per-tensor FP8 scale of the readout independent of the pads).
-template <class Tag, class Gates, int CPL>
+template <class Tag, class Gates, int CPL, bool kTokenPairs = false>
 __device__ __forceinline__ void prefill_tile(typename Storage<Tag>::T* __restrict__ pool,
                                              const int* __restrict__ slot_idx,
                                              const float* __restrict__ q,
@@ -391,12 +391,39 @@ __device__ __forceinline__ void prefill_tile(typename Storage<Tag>::T* __restric
     if (t0 + kStage < len)
       load_stage<kW>(pre, L.wave, L.lane, gates, q, k, v, b, h, g, H, G, T, t0 + kStage,
                      min(kStage, len - t0 - kStage));
-    for (int j = 0; j < n; ++j) {
+    float* yt = y + (((size_t)b * T + t0) * H + h) * kHD + L.col0;
+    const size_t y_tok = (size_t)H * kHD;
+    int j = 0;
+    if constexpr (kTokenPairs) {
+      // Two tokens per iteration, both y stores after both tokens, so the two
+      // token bodies form one basic block the scheduler can interleave (the
+      // second token's loads and kv chain with the first's readout). Used by
+      // the one-column layout of gdn_prefill_kernel: it is latency-bound (a
+      // wave issues VALU about half its cycles) and runs at most one
+      // workgroup per CU, so the extra registers cost nothing. Measured:
+      // config 4's 4 x 256 tokens 0.189 -> 0.181 ms, one 512-token row
+      // 0.340 -> 0.316 ms. In the planned kernel, whose register count both
+      // layouts set and which may hold two workgroups per CU, it was 8-20%
+      // slower.
+      for (; j + 1 < n; j += 2) {
+        TokenIn<CPL> in0, in1;
+        read_token<CPL>(st, j, r0, L.col0, in0);
+        read_token<CPL>(st, j + 1, r0, L.col0, in1);
+        float y0[CPL], y1[CPL];
+        scan_token<Tag, CPL, true>(S, in0.kh, in0.qh, in0.v, in0.alpha, in0.beta, y0);
+        scan_token<Tag, CPL, true>(S, in1.kh, in1.qh, in1.v, in1.alpha, in1.beta, y1);
+        if (L.stores_y()) {
+          storeN<CPL>(yt + j * y_tok, y0);
+          storeN<CPL>(yt + (j + 1) * y_tok, y1);
+        }
+      }
+    }
+    for (; j < n; ++j) {
       TokenIn<CPL> in;
       read_token<CPL>(st, j, r0, L.col0, in);
       float yy[CPL];
       scan_token<Tag, CPL>(S, in.kh, in.qh, in.v, in.alpha, in.beta, yy);
-      if (L.stores_y()) storeN<CPL>(y + (((size_t)b * T + t0 + j) * H + h) * kHD + L.col0, yy);
+      if (L.stores_y()) storeN<CPL>(yt + j * y_tok, yy);
     }
     __syncthreads();
   }
@@ -434,8 +461,8 @@ gdn_prefill_kernel(typename Storage<Tag>::T* __restrict__ pool,
   const int b = tile_id / H;
   const int h = tile_id - b * H;
   __shared__ StageLds st;
-  prefill_tile<Tag, Gates, CPL>(pool, slot_idx, q, k, v, gates, y, H, G, heads_per_group, T, b,
-                                h, part, gates.row_len(b, T), st);
+  prefill_tile<Tag, Gates, CPL, CPL == 1>(pool, slot_idx, q, k, v, gates, y, H, G,
+                                          heads_per_group, T, b, h, part, gates.row_len(b, T), st);
 }
 
 // Ragged batches: the rows' live lengths decide the layout. Every workgroup

@@ -206,6 +206,16 @@ struct Row<F32, 1> {
   __device__ __forceinline__ void set1(float x) { d = x; }
 };
 
+// x as an opaque fp32 register value: a narrowing of the result then starts
+// from the rounded fp32 value. Without it the backend can fuse the producing
+// fma with a single-element fp16 narrowing into one mixed-precision fma that
+// rounds once, straight to 16 bits (seen when two scan tokens share a basic
+// block). Costs a register copy when x has another use.
+__device__ __forceinline__ float opaque(float x) {
+  asm("" : "+v"(x));
+  return x;
+}
+
 struct RowHalf1 {
   uint32_t raw;  // the element in bits 0..15
   __device__ __forceinline__ void load_nt(const uint16_t* p) {
@@ -666,7 +676,9 @@ __device__ __forceinline__ void gdn_token(const LaneMap<CPL, kSplit>& L,
 // w * 32 + rg + 4 i), in the scan layout: the decode token's arithmetic, each
 // element's operations in the decode's order. kh / qh hold the row block's 32
 // normalised key / query entries in row order.
-template <class Tag, int CPL>
+// kOpaqueNarrow: narrow each new state element through opaque() (for callers
+// whose code shape lets the backend contract the narrowing).
+template <class Tag, int CPL, bool kOpaqueNarrow = false>
 __device__ __forceinline__ void scan_token(Row<Tag, CPL> (&S)[kRowGroups][kRowsPerLane],
                                            const float (&kh)[kRowsPerWave],
                                            const float (&qh)[kRowsPerWave],
@@ -698,7 +710,7 @@ __device__ __forceinline__ void scan_token(Row<Tag, CPL> (&S)[kRowGroups][kRowsP
       const int r = rg + kRowGroups * i;
       if constexpr (CPL == 1) {
         const float n0 = fmaf(alpha, S[rg][i].get(0), kh[r] * delta[0]);
-        S[rg][i].set1(n0);
+        S[rg][i].set1(kOpaqueNarrow ? opaque(n0) : n0);
         ch[rg][0] = fmaf(n0, qh[r], ch[rg][0]);
       } else {
 #pragma unroll
