@@ -108,9 +108,12 @@ def make_workload(torch, n_pools, seed=0):
     return pools, slot_maps, inputs, A, dt_bias
 
 
-def time_steps(torch, kern, work, steps, warmup):
+def time_steps(torch, kern, work, steps, warmup, spread_reps=0):
     """Capture `steps` decode launches (step i on pool i % P) in one graph,
-    replay it once between synchronisations; returns seconds for all steps."""
+    replay it once between synchronisations; returns seconds for all steps.
+    With spread_reps > 0 the graph is then replayed that many more times, each
+    timed alone, and the per-step p10 / p50 / p90 microseconds of those replays
+    are returned too (the timed replay above stays the reported figure)."""
     pools, slot_maps, inputs, A, dtb = work
     P = len(pools)
 
@@ -135,7 +138,21 @@ def time_steps(torch, kern, work, steps, warmup):
     graph.replay()
     end.record()
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / 1e3
+    total = start.elapsed_time(end) / 1e3
+    if spread_reps <= 0:
+        return total
+    per_step = []
+    for _ in range(spread_reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        graph.replay()
+        b.record()
+        torch.cuda.synchronize()
+        per_step.append(a.elapsed_time(b) * 1e3 / steps)
+    per_step.sort()
+    q = lambda f: round(per_step[min(len(per_step) - 1, int(f * len(per_step)))], 3)
+    return total, {"reps": spread_reps, "steps_per_rep": steps, "p10_us": q(0.1),
+                   "p50_us": q(0.5), "p90_us": q(0.9)}
 
 
 def copy_bandwidth(torch, nbytes=2 ** 30):
@@ -568,7 +585,7 @@ def main():
     kern = load_gdn()
     n_cold = max(2, math.ceil(COLD_BYTES / (SLOTS * H * D * D * 2)))
     work = make_workload(torch, n_cold)
-    t_cold = time_steps(torch, kern, work, args.steps, args.warmup)
+    t_cold, spread = time_steps(torch, kern, work, args.steps, args.warmup, spread_reps=30)
     hot_work = tuple([x[:1] for x in work[:3]] + list(work[3:]))
     t_hot = time_steps(torch, kern, hot_work, args.steps, args.warmup)
     del work, hot_work
@@ -604,6 +621,8 @@ def main():
                      "traffic": traffic},
         "achieved_gbs": round(achieved, 1),
         "hbm_frac": round(achieved / HBM_PEAK_GBS, 4),
+        # 30 further replays of the same graph, each timed alone: per-step spread
+        "spread_us_per_step": spread,
         "hot_steps_per_s": round(args.steps / t_hot, 2),
         "hot_achieved_gbs": round(STEP_BYTES / (t_hot / args.steps) / 1e9, 1),
         "copy_gbs": round(copy_gbs, 1),
