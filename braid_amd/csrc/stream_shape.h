@@ -50,8 +50,10 @@ inline int env_override(const char* name) {
 // cus: CUs of the device (0 if unknown: no large-launch choices);
 // narrow: 16-bit tiles; static_lds: the kernel's own LDS bytes.
 inline StreamShape stream_shape(long n_tiles, int cus, bool narrow, size_t static_lds) {
-  static const int remap_env = env_override("BRAID_DECODE_XCD_REMAP");
-  static const int cap_env = env_override("BRAID_DECODE_WGS_PER_CU");
+  // Read per launch (two getenv calls), so a process can change them between
+  // launches.
+  const int remap_env = env_override("BRAID_DECODE_XCD_REMAP");
+  const int cap_env = env_override("BRAID_DECODE_WGS_PER_CU");
   const bool large = cus > 0 && n_tiles >= 12L * cus;
   StreamShape s{0, 0};
   const bool remap = remap_env >= 0 ? remap_env > 0 : large;

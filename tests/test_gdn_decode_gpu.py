@@ -287,3 +287,48 @@ def test_state_narrowing_rounds_to_nearest_even_exactly(kern, dt):
         assert np.array_equal(got.view(np.uint16), expected.view(np.uint16)), (
             f"{int((got.view(np.uint16) != expected.view(np.uint16)).sum())} elements "
             "rounded differently from round-to-nearest-even")
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16, torch.float32],
+                         ids=["f16-pool", "bf16-pool", "f32-pool"])
+def test_launch_shapes_give_identical_bits(kern, dt, monkeypatch):
+    """A launch of at least 12 tiles per CU walks XCD-contiguous tile ranges
+    and, on a 16-bit pool, keeps three workgroups resident per CU. Each tile is
+    still one workgroup's work, so every launch shape (forced through the
+    override variables) must leave the same pool and y bits; the default one is
+    also checked against the oracle on a sample of rows."""
+    H, G = 32, 16
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    B = max(128, -(-12 * cus // H))
+    B += (-B) % 8
+    slots = torch.randperm(B + 16, generator=torch.Generator().manual_seed(3))[:B]
+    slots = slots.to(torch.int32).to(DEV)
+    inp = decode_inputs(B, H=H, G=G, seed=21)
+    a_raw, b_raw, A, dt_bias = raw_gates((B, H), H, torch.bfloat16, seed=22)
+    base = pool(B + 16, H=H, dtype=dt, seed=23)
+    results = {}
+    for label, remap, cap in (("default", None, None), ("dispatch order", "0", "0"),
+                              ("remap only", "1", "0"), ("cap 2", "1", "2"),
+                              ("cap 4, dispatch order", "0", "4")):
+        for name, val in (("BRAID_DECODE_XCD_REMAP", remap), ("BRAID_DECODE_WGS_PER_CU", cap)):
+            if val is None:
+                monkeypatch.delenv(name, raising=False)
+            else:
+                monkeypatch.setenv(name, val)
+        p = base.clone()
+        y = torch.empty(B, H, 128, device=DEV)
+        kern.gdn_decode_raw(p, slots, inp["q"], inp["k"], inp["v"], a_raw, b_raw, A, dt_bias, y)
+        torch.cuda.synchronize()
+        results[label] = (p, y)
+    p0, y0 = results["default"]
+    for label, (p, y) in results.items():
+        assert torch.equal(p.view(torch.uint8), p0.view(torch.uint8)), label
+        assert torch.equal(y, y0), label
+    rows = [0, B // 2, B - 1]
+    sub = slots[rows].cpu().numpy()
+    ref_pool = to_np_pool(base)
+    alpha, beta = torch_gates(a_raw, b_raw, A, dt_bias)
+    n = {k: v[rows].cpu().numpy() for k, v in inp.items()}
+    y_ref = oracle.gdn_decode(ref_pool, sub, n["q"], n["k"], n["v"],
+                              alpha[rows].cpu().numpy(), beta[rows].cpu().numpy(), KIND[dt])
+    np.testing.assert_allclose(y0[rows].cpu().numpy(), y_ref, rtol=RTOL, atol=ATOL)
