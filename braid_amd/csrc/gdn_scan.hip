@@ -338,6 +338,30 @@ __device__ __forceinline__ void read_token(const StageLds& st, int j, int r0, in
   }
 }
 
+// The quarter layout's token: its 16 rows' k_hat / q_hat (rows r0 + 2 rgh +
+// rgl + 4 i: a float2 per i), its column's v, and the gates.
+struct TokenInQ {
+  float kh[2][kRowsPerLane], qh[2][kRowsPerLane];
+  float v, alpha, beta;
+};
+
+__device__ __forceinline__ void read_token_quarter(const StageLds& st, int j, int r0, int col0,
+                                                   TokenInQ& t) {
+  const float2 ab = *reinterpret_cast<const float2*>(&st.gate[j][0]);
+  t.alpha = ab.x;
+  t.beta = ab.y;
+  t.v = st.v[j][col0];
+#pragma unroll
+  for (int i = 0; i < kRowsPerLane; ++i) {
+    const float2 k2 = *reinterpret_cast<const float2*>(&st.qk[j][1][r0 + kRowGroups * i]);
+    const float2 q2 = *reinterpret_cast<const float2*>(&st.qk[j][0][r0 + kRowGroups * i]);
+    t.kh[0][i] = k2.x;
+    t.kh[1][i] = k2.y;
+    t.qh[0][i] = q2.x;
+    t.qh[1][i] = q2.y;
+  }
+}
+
 // The live tokens of one tile, with the state resident in registers. Scan
 // layout (ScanMap): four waves; a lane holds the 32 rows of its row block for
 // CPL columns; the column sums finish in-lane and over the four row blocks
@@ -353,7 +377,7 @@ __device__ __forceinline__ void read_token(const StageLds& st, int j, int r0, in
 // into +0. y at the pad positions [len, T) is written as 0 (the reference
 // leaves arbitrary values there that nothing reads; zeros also keep a later
 // per-tensor FP8 scale of the readout independent of the pads).
-template <class Tag, class Gates, int CPL, bool kTokenPairs = false>
+template <class Tag, class Gates, int Layout, bool kTokenPairs = false>
 __device__ __forceinline__ void prefill_tile(typename Storage<Tag>::T* __restrict__ pool,
                                              const int* __restrict__ slot_idx,
                                              const float* __restrict__ q,
@@ -362,22 +386,27 @@ __device__ __forceinline__ void prefill_tile(typename Storage<Tag>::T* __restric
                                              float* __restrict__ y, int H, int G,
                                              int heads_per_group, int T, int b, int h, int part,
                                              int len, StageLds& st) {
-  using LM = ScanMap<CPL>;
+  using LM = typename ScanLayoutOf<Layout>::type;
+  constexpr int CPL = LM::kCPL;
+  constexpr int kLRG = LM::kLaneRowGroups;
   using ST = typename Storage<Tag>::T;
   const int g = h / heads_per_group;
   const LM L(threadIdx.x, part);
   const int slot = slot_idx[b];
   ST* tile = pool + ((size_t)slot * H + h) * (kSS * kHD) + L.col0;
 
-  Row<Tag, CPL> S[kRowGroups][kRowsPerLane];
+  Row<Tag, CPL> S[kLRG][kRowsPerLane];
 #pragma unroll
-  for (int rg = 0; rg < kRowGroups; ++rg) {
+  for (int rg = 0; rg < kLRG; ++rg) {
 #pragma unroll
     for (int i = 0; i < kRowsPerLane; ++i) S[rg][i].load_nt(tile + (size_t)L.row(rg, i) * kHD);
   }
 
   constexpr int kW = LM::kWaves;
-  const int r0 = L.w * kRowsPerWave;
+  // The lane's first row: its row block's (and, in the quarter layout, its
+  // row-group half's).
+  int r0 = L.w * kRowsPerWave;
+  if constexpr (Layout == 4) r0 += 2 * L.rgh;
   StageRegs<kW> pre;
   // (Loads nothing when len == 0; a branch around it costs ~30 VGPRs.)
   load_stage<kW>(pre, L.wave, L.lane, gates, q, k, v, b, h, g, H, G, T, 0, min(kStage, len));
@@ -394,7 +423,29 @@ __device__ __forceinline__ void prefill_tile(typename Storage<Tag>::T* __restric
     float* yt = y + (((size_t)b * T + t0) * H + h) * kHD + L.col0;
     const size_t y_tok = (size_t)H * kHD;
     int j = 0;
-    if constexpr (kTokenPairs) {
+    if constexpr (Layout == 4) {
+      if constexpr (kTokenPairs) {
+        for (; j + 1 < n; j += 2) {
+          TokenInQ in0, in1;
+          read_token_quarter(st, j, r0, L.col0, in0);
+          read_token_quarter(st, j + 1, r0, L.col0, in1);
+          float y0[1], y1[1];
+          scan_token_quarter<Tag, true>(S, in0.kh, in0.qh, in0.v, in0.alpha, in0.beta, y0[0]);
+          scan_token_quarter<Tag, true>(S, in1.kh, in1.qh, in1.v, in1.alpha, in1.beta, y1[0]);
+          if (L.stores_y()) {
+            storeN<1>(yt + j * y_tok, y0);
+            storeN<1>(yt + (j + 1) * y_tok, y1);
+          }
+        }
+      }
+      for (; j < n; ++j) {
+        TokenInQ in;
+        read_token_quarter(st, j, r0, L.col0, in);
+        float yy[1];
+        scan_token_quarter<Tag>(S, in.kh, in.qh, in.v, in.alpha, in.beta, yy[0]);
+        if (L.stores_y()) storeN<1>(yt + j * y_tok, yy);
+      }
+    } else if constexpr (kTokenPairs) {
       // Two tokens per iteration, both y stores after both tokens, so the two
       // token bodies form one basic block the scheduler can interleave (the
       // second token's loads and kv chain with the first's readout). Used by
@@ -418,18 +469,20 @@ __device__ __forceinline__ void prefill_tile(typename Storage<Tag>::T* __restric
         }
       }
     }
-    for (; j < n; ++j) {
-      TokenIn<CPL> in;
-      read_token<CPL>(st, j, r0, L.col0, in);
-      float yy[CPL];
-      scan_token<Tag, CPL>(S, in.kh, in.qh, in.v, in.alpha, in.beta, yy);
-      if (L.stores_y()) storeN<CPL>(yt + j * y_tok, yy);
+    if constexpr (Layout != 4) {
+      for (; j < n; ++j) {
+        TokenIn<CPL> in;
+        read_token<CPL>(st, j, r0, L.col0, in);
+        float yy[CPL];
+        scan_token<Tag, CPL>(S, in.kh, in.qh, in.v, in.alpha, in.beta, yy);
+        if (L.stores_y()) storeN<CPL>(yt + j * y_tok, yy);
+      }
     }
     __syncthreads();
   }
 
 #pragma unroll
-  for (int rg = 0; rg < kRowGroups; ++rg) {
+  for (int rg = 0; rg < kLRG; ++rg) {
 #pragma unroll
     for (int i = 0; i < kRowsPerLane; ++i) S[rg][i].store_nt(tile + (size_t)L.row(rg, i) * kHD);
   }
@@ -448,21 +501,22 @@ __device__ __forceinline__ void prefill_tile(typename Storage<Tag>::T* __restric
 
 // One tile (CPL = 2) or one half tile (CPL = 1, kParts = 2) per workgroup:
 // blockIdx.x = (b * H + h) * kParts + part.
-template <class Tag, class Gates, int CPL>
-__global__ void __launch_bounds__(64 * ScanMap<CPL>::kWaves)
+template <class Tag, class Gates, int Layout>
+__global__ void __launch_bounds__(64 * ScanLayoutOf<Layout>::type::kWaves)
 gdn_prefill_kernel(typename Storage<Tag>::T* __restrict__ pool,
                    const int* __restrict__ slot_idx,
                    const float* __restrict__ q, const float* __restrict__ k,
                    const float* __restrict__ v, Gates gates, float* __restrict__ y,
                    int H, int G, int heads_per_group, int T) {
-  using LM = ScanMap<CPL>;
+  using LM = typename ScanLayoutOf<Layout>::type;
   const int tile_id = blockIdx.x / LM::kParts;
   const int part = blockIdx.x - tile_id * LM::kParts;
   const int b = tile_id / H;
   const int h = tile_id - b * H;
   __shared__ StageLds st;
-  prefill_tile<Tag, Gates, CPL, CPL == 1>(pool, slot_idx, q, k, v, gates, y, H, G,
-                                          heads_per_group, T, b, h, part, gates.row_len(b, T), st);
+  prefill_tile<Tag, Gates, Layout, Layout != 2>(pool, slot_idx, q, k, v, gates, y, H, G,
+                                                heads_per_group, T, b, h, part,
+                                                gates.row_len(b, T), st);
 }
 
 // Ragged batches: the rows' live lengths decide the layout. Every workgroup
@@ -605,39 +659,45 @@ int launch_decode(void* pool, int pool_dtype, const int32_t* slot_idx, int B, in
 }
 
 // Prefill layout of a launch:
-//   1: one column per lane for every tile (two workgroups per tile), when that
-//      still leaves no CU with a second workgroup;
+//   4: the quarter layout (one column and 16 rows per lane, four workgroups
+//      per tile), when that still leaves no CU with a second workgroup;
+//   1: one column per lane for every tile (two workgroups per tile), likewise;
 //   2: two columns per lane for every tile;
 //   0: planned per row from seq_lens (gdn_prefill_planned_kernel), for larger
 //      ragged batches.
-// BRAID_PREFILL_COLS (1, 2, or 0 for planned when seq_lens is given)
-// overrides the choice.
+// Measured (MI355X, 256 CUs): one 512-token row 0.315 ms in layout 1, 0.225 ms
+// in layout 4; rows (300, 700) 0.425 -> 0.301 ms; config 4's 128 tiles, where
+// layout 4 would put two workgroups on every CU, 0.183 in layout 1 against
+// 0.190 ms. BRAID_PREFILL_COLS (1, 2, 4, or 0 for planned when seq_lens is
+// given) overrides the choice.
 int prefill_layout(int n_tiles, int B, bool ragged, int cus) {
   const char* env = std::getenv("BRAID_PREFILL_COLS");
-  if (env != nullptr && (std::atoi(env) == 1 || std::atoi(env) == 2)) return std::atoi(env);
+  if (env != nullptr && (std::atoi(env) == 1 || std::atoi(env) == 2 || std::atoi(env) == 4))
+    return std::atoi(env);
   if (env != nullptr && env[0] == '0' && ragged && B <= kMaxPlanRows) return 0;
+  if (cus > 0 && 4 * n_tiles <= cus) return 4;
   if (cus > 0 && 2 * n_tiles <= cus) return 1;
   return ragged && B <= kMaxPlanRows && cus > 0 ? 0 : 2;
 }
 
-template <class Gates, int CPL>
+template <class Gates, int Layout>
 void launch_prefill_cols(void* pool, int pool_dtype, const int32_t* slot_idx, int B, int T,
                          int H, int G, const float* q, const float* k, const float* v,
                          Gates gates, float* y, hipStream_t stream) {
-  using LM = ScanMap<CPL>;
+  using LM = typename ScanLayoutOf<Layout>::type;
   const dim3 grid((unsigned)B * (unsigned)H * LM::kParts), block(64 * LM::kWaves);
   const int hpg = H / G;
   switch (pool_dtype) {
     case BRAID_F32:
-      gdn_prefill_kernel<F32, Gates, CPL><<<grid, block, 0, stream>>>(
+      gdn_prefill_kernel<F32, Gates, Layout><<<grid, block, 0, stream>>>(
           static_cast<float*>(pool), slot_idx, q, k, v, gates, y, H, G, hpg, T);
       break;
     case BRAID_F16:
-      gdn_prefill_kernel<F16, Gates, CPL><<<grid, block, 0, stream>>>(
+      gdn_prefill_kernel<F16, Gates, Layout><<<grid, block, 0, stream>>>(
           static_cast<uint16_t*>(pool), slot_idx, q, k, v, gates, y, H, G, hpg, T);
       break;
     default:
-      gdn_prefill_kernel<BF16, Gates, CPL><<<grid, block, 0, stream>>>(
+      gdn_prefill_kernel<BF16, Gates, Layout><<<grid, block, 0, stream>>>(
           static_cast<uint16_t*>(pool), slot_idx, q, k, v, gates, y, H, G, hpg, T);
       break;
   }
@@ -672,7 +732,10 @@ int launch_prefill(void* pool, int pool_dtype, const int32_t* slot_idx, int B, i
                    float* y, hipStream_t stream) {
   const int cus = device_cus();
   const int layout = prefill_layout(B * H, B, gates.ragged(), cus);
-  if (layout == 1)
+  if (layout == 4)
+    launch_prefill_cols<Gates, 4>(pool, pool_dtype, slot_idx, B, T, H, G, q, k, v, gates, y,
+                                  stream);
+  else if (layout == 1)
     launch_prefill_cols<Gates, 1>(pool, pool_dtype, slot_idx, B, T, H, G, q, k, v, gates, y,
                                   stream);
   else if (layout == 2)

@@ -478,6 +478,8 @@ __device__ __forceinline__ void store_row(const Row<Tag, CPL>& r, const LaneMap<
 // half the per-token work.
 template <int CPL>
 struct ScanMap {
+  static constexpr int kCPL = CPL;
+  static constexpr int kLaneRowGroups = kRowGroups;  // a lane holds all 32 rows of its block
   static constexpr int kColsPerWave = 16 * CPL;
   static constexpr int kWavesPerTile = kHD / kColsPerWave;
   static constexpr int kWaves = 4;  // per workgroup
@@ -496,6 +498,53 @@ struct ScanMap {
   // Row block 0's lanes write the column totals (every lane holds them).
   __device__ __forceinline__ bool stores_y() const { return w == 0; }
 };
+
+// Quarter scan layout: one column and two of the four row groups per lane, so
+// a lane holds 16 rows and a tile spreads over four workgroups of four waves
+// (8 columns per wave). Lane l: column cc = l % 8, row-group half
+// rgh = (l / 8) % 2 (row groups 2 rgh and 2 rgh + 1), row block w = l / 16.
+// Column totals: in-lane (rg 2rgh + rg 2rgh+1), then lane xor 8 gives
+// (rg0 + rg1) + (rg2 + rg3), then xor 16 and xor 32 as in the other layouts,
+// which is the decode's order.
+struct ScanMapQuarter {
+  static constexpr int kCPL = 1;
+  static constexpr int kLaneRowGroups = 2;
+  static constexpr int kColsPerWave = 8;
+  static constexpr int kWavesPerTile = kHD / kColsPerWave;
+  static constexpr int kWaves = 4;  // per workgroup
+  static constexpr int kParts = kWavesPerTile / kWaves;
+  int wave, lane, cc, rgh, w, col0;
+  __device__ __forceinline__ ScanMapQuarter(int tid, int part) {
+    lane = tid & 63;
+    wave = tid >> 6;
+    cc = lane & 7;
+    rgh = (lane >> 3) & 1;
+    w = lane >> 4;
+    col0 = (part * kWaves + wave) * kColsPerWave + cc;
+  }
+  // rgl: the lane's row group 0 or 1 (row group 2 rgh + rgl).
+  __device__ __forceinline__ int row(int rgl, int i) const {
+    return w * kRowsPerWave + 2 * rgh + rgl + kRowGroups * i;
+  }
+  __device__ __forceinline__ bool stores_y() const { return w == 0 && rgh == 0; }
+};
+
+// Scan layout of a prefill launch by code: 1 and 2 columns per lane
+// (ScanMap), 4 for the quarter layout (four workgroups per tile).
+template <int L>
+struct ScanLayoutOf {
+  using type = ScanMap<L>;
+};
+template <>
+struct ScanLayoutOf<4> {
+  using type = ScanMapQuarter;
+};
+
+// Sum with the partner lane xor 8 (within each 16-lane row): DPP row_ror:8.
+__device__ __forceinline__ float add_xor8(float v) {
+  const int p = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xf, 0xf, false);
+  return v + __int_as_float(p);
+}
 
 // Partner exchanges of the scan layout's tree, all VALU (no LDS): lane
 // xor 16 and xor 32 through gfx950's v_permlane16_swap / v_permlane32_swap.
@@ -727,6 +776,37 @@ __device__ __forceinline__ void scan_token(Row<Tag, CPL> (&S)[kRowGroups][kRowsP
 #pragma unroll
   for (int c = 0; c < CPL; ++c)
     y[c] = scan_column_sum(ch[0][c], ch[1][c], ch[2][c], ch[3][c]) * kYScale;
+}
+
+// One token of the quarter layout on this lane's 16 rows x 1 column: S[rgl][i]
+// is row w * 32 + 2 rgh + rgl + 4 i, kh / qh hold the same rows. Each
+// element's operations are scan_token's (and so the decode's), in the same
+// order; the column totals follow the layout's tree.
+template <class Tag, bool kOpaqueNarrow = false>
+__device__ __forceinline__ void scan_token_quarter(Row<Tag, 1> (&S)[2][kRowsPerLane],
+                                                   const float (&kh)[2][kRowsPerLane],
+                                                   const float (&qh)[2][kRowsPerLane], float v,
+                                                   float alpha, float beta, float& y) {
+  float ch[2];
+#pragma unroll
+  for (int g = 0; g < 2; ++g) {
+    ch[g] = S[g][0].get(0) * kh[g][0];
+#pragma unroll
+    for (int i = 1; i < kRowsPerLane; ++i) ch[g] = fmaf(S[g][i].get(0), kh[g][i], ch[g]);
+  }
+  const float kv = add_xor32(add_xor16(add_xor8(ch[0] + ch[1])));
+  const float delta = (v - alpha * kv) * beta;
+#pragma unroll
+  for (int g = 0; g < 2; ++g) {
+    ch[g] = 0.f;
+#pragma unroll
+    for (int i = 0; i < kRowsPerLane; ++i) {
+      const float n0 = fmaf(alpha, S[g][i].get(0), kh[g][i] * delta);
+      S[g][i].set1(kOpaqueNarrow ? opaque(n0) : n0);
+      ch[g] = fmaf(n0, qh[g][i], ch[g]);
+    }
+  }
+  y = add_xor32(add_xor16(add_xor8(ch[0] + ch[1]))) * kYScale;
 }
 
 // Computes one token's gates ONCE per tile and leaves them in lds.gate for
