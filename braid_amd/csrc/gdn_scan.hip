@@ -9,6 +9,7 @@
 // it back; prefill loads it once, runs T tokens with the tile resident in
 // registers (in the pool's storage type) and stores it once. Reference behaviour: braid/kernels/csrc/gdn_decode.cu:156-272 (decode)
 // and :467-551 (prefill); entry-point contracts :313-441 and :553-699.
+#include <algorithm>
 #include <atomic>
 #include <cstdlib>
 #include <type_traits>
@@ -519,19 +520,24 @@ gdn_prefill_kernel(typename Storage<Tag>::T* __restrict__ pool,
                                                 gates.row_len(b, T), st);
 }
 
-// Ragged batches: the rows' live lengths decide the layout. Every workgroup
-// derives the same plan from seq_lens:
+// Ragged batches of up to four tiles per CU: the rows' live lengths decide
+// the layout. Every workgroup derives the same plan from seq_lens:
 //   * rows ranked by live length, longest first (ties by row index);
-//   * the rows longer than kSplitFrac of the longest are "long": each of their
-//     tiles is split over two workgroups (one column per lane), which cuts the
-//     serial per-token latency by about a quarter; the rest run whole (two
-//     columns per lane). Splitting pays only if every long row is split, so if
-//     that would need more than max_wgs workgroups, no row is split.
-//   * workgroup order: the long rows' half tiles first, then the other rows'
-//     tiles, longest rows first, so the longest chains start on CUs of their
-//     own and the short rows fill in. Workgroups beyond the plan return.
-// A row's tiles compute the same bits in either layout.
-constexpr float kSplitFrac = 0.8f;
+//   * three tiers by rank: the first n4 rows run in the quarter layout (four
+//     workgroups per tile), the next n2 split over two workgroups (one column
+//     per lane), the rest whole (two columns per lane). A tier's per-token
+//     time, relative to a whole tile's, is about kSplitCost and kQuarterCost
+//     (measured on single rows), so splitting shortens a row's chain but costs
+//     more workgroup time in all. (n4, n2) minimise the estimated makespan:
+//     the larger of the critical path and the total workgroup time over the
+//     CUs, with at most one extra workgroup per CU (the first plan found wins
+//     ties);
+//   * workgroup order: quarter tiles, then split tiles, then whole tiles,
+//     longest rows first within each, so the longest chains start on CUs of
+//     their own and the short rows fill in. Workgroups beyond the plan return.
+// A row's tiles compute the same bits in any layout.
+constexpr float kSplitCost = 0.745f;
+constexpr float kQuarterCost = 0.47f;
 constexpr int kMaxPlanRows = 1024;
 
 template <class Tag, class Gates>
@@ -540,11 +546,12 @@ gdn_prefill_planned_kernel(typename Storage<Tag>::T* __restrict__ pool,
                            const int* __restrict__ slot_idx,
                            const float* __restrict__ q, const float* __restrict__ k,
                            const float* __restrict__ v, Gates gates, float* __restrict__ y,
-                           int B, int H, int G, int heads_per_group, int T, int max_wgs) {
+                           int B, int H, int G, int heads_per_group, int T, int cus,
+                           int max_extra) {
   __shared__ StageLds st;
   __shared__ int lens[kMaxPlanRows];
   __shared__ int order[kMaxPlanRows];  // row of each rank
-  __shared__ int n_long;
+  __shared__ int plan[2];  // n4, n2
   for (int r = threadIdx.x; r < B; r += blockDim.x) lens[r] = gates.row_len(r, T);
   __syncthreads();
   for (int r = threadIdx.x; r < B; r += blockDim.x) {
@@ -555,25 +562,67 @@ gdn_prefill_planned_kernel(typename Storage<Tag>::T* __restrict__ pool,
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    const float cut = kSplitFrac * (float)lens[order[0]];
-    int s = 0;
-    while (s < B && (float)lens[order[s]] > cut) ++s;
-    n_long = ((B + s) * H <= max_wgs) ? s : 0;
+    // Estimated makespan of a plan, in whole-tile token times: the larger of
+    // its critical path (each tier's longest row x the tier's per-token cost)
+    // and its total workgroup time spread over the CUs (a quarter tile costs
+    // 4 kQuarterCost of a whole tile's time, a split one 2 kSplitCost). At
+    // most max_extra workgroups beyond one per tile: 3 H per quarter row, H
+    // per split row.
+    const int extra = max_extra / H;
+    const float per_cu = (float)H / (float)cus;
+    float total = 0.f;
+    for (int r = 0; r < B; ++r) total += (float)lens[r];
+    float best = fmaxf((float)lens[order[0]], total * per_cu);
+    int b4 = 0, b2 = 0;
+    float sum4 = 0.f;  // lengths of the quarter rows
+    for (int n4 = 0; n4 <= B && 3 * n4 <= extra; ++n4) {
+      if (n4 > 0) sum4 += (float)lens[order[n4 - 1]];
+      const float m4 = n4 > 0 ? kQuarterCost * (float)lens[order[0]] : 0.f;
+      float sum2 = 0.f;  // lengths of the split rows
+      for (int n2 = 0; n4 + n2 <= B && 3 * n4 + n2 <= extra; ++n2) {
+        if (n2 > 0) sum2 += (float)lens[order[n4 + n2 - 1]];
+        const float fixed = fmaxf(m4, n2 > 0 ? kSplitCost * (float)lens[order[n4]] : 0.f);
+        const float whole = n4 + n2 < B ? (float)lens[order[n4 + n2]] : 0.f;
+        const float work = (total + (4.f * kQuarterCost - 1.f) * sum4 +
+                            (2.f * kSplitCost - 1.f) * sum2) * per_cu;
+        const float m = fmaxf(fmaxf(fixed, whole), work);
+        if (m < best) {
+          best = m;
+          b4 = n4;
+          b2 = n2;
+        }
+        // Once the whole tier no longer sets the critical path, splitting
+        // more rows cannot lower the estimate.
+        if (whole <= fixed) break;
+      }
+    }
+    plan[0] = b4;
+    plan[1] = b2;
   }
   __syncthreads();
-  const int S = n_long;
-  const int i = blockIdx.x;
-  if (i < 2 * S * H) {
-    const int rank = i / (2 * H), rem = i - rank * 2 * H;
+  const int n4 = plan[0], n2 = plan[1];
+  int i = blockIdx.x;
+  if (i < 4 * n4 * H) {
+    const int rank = i / (4 * H), rem = i - rank * 4 * H;
+    const int b = order[rank];
+    prefill_tile<Tag, Gates, 4, true>(pool, slot_idx, q, k, v, gates, y, H, G, heads_per_group, T,
+                                      b, rem >> 2, rem & 3, lens[b], st);
+    return;
+  }
+  i -= 4 * n4 * H;
+  if (i < 2 * n2 * H) {
+    const int rank = n4 + i / (2 * H), rem = i - (rank - n4) * 2 * H;
     const int b = order[rank];
     prefill_tile<Tag, Gates, 1>(pool, slot_idx, q, k, v, gates, y, H, G, heads_per_group, T, b,
                                 rem >> 1, rem & 1, lens[b], st);
-  } else if (i - 2 * S * H < (B - S) * H) {
-    const int w = i - 2 * S * H;
-    const int rank = S + w / H;
+    return;
+  }
+  i -= 2 * n2 * H;
+  if (i < (B - n4 - n2) * H) {
+    const int rank = n4 + n2 + i / H;
     const int b = order[rank];
     prefill_tile<Tag, Gates, 2>(pool, slot_idx, q, k, v, gates, y, H, G, heads_per_group, T, b,
-                                w - (w / H) * H, 0, lens[b], st);
+                                i - (i / H) * H, 0, lens[b], st);
   }
 }
 
@@ -677,7 +726,7 @@ int prefill_layout(int n_tiles, int B, bool ragged, int cus) {
   if (env != nullptr && env[0] == '0' && ragged && B <= kMaxPlanRows) return 0;
   if (cus > 0 && 4 * n_tiles <= cus) return 4;
   if (cus > 0 && 2 * n_tiles <= cus) return 1;
-  return ragged && B <= kMaxPlanRows && cus > 0 ? 0 : 2;
+  return ragged && B <= kMaxPlanRows && cus > 0 && n_tiles <= 4 * cus ? 0 : 2;
 }
 
 template <class Gates, int Layout>
@@ -707,21 +756,26 @@ template <class Gates>
 void launch_prefill_planned(void* pool, int pool_dtype, const int32_t* slot_idx, int B, int T,
                             int H, int G, const float* q, const float* k, const float* v,
                             Gates gates, float* y, int cus, hipStream_t stream) {
-  // Room for every tile plus a split of every row; the plan uses what it needs.
-  const dim3 grid((unsigned)(2 * B * H)), block(256);
-  const int hpg = H / G, max_wgs = cus + cus / 4;
+  // At most one extra workgroup per CU for split tiles; the grid has room for
+  // whatever the plan uses (the rest return at once).
+  const int max_extra = std::min(cus, 3 * B * H);
+  const dim3 grid((unsigned)(B * H + max_extra)), block(256);
+  const int hpg = H / G;
   switch (pool_dtype) {
     case BRAID_F32:
       gdn_prefill_planned_kernel<F32, Gates><<<grid, block, 0, stream>>>(
-          static_cast<float*>(pool), slot_idx, q, k, v, gates, y, B, H, G, hpg, T, max_wgs);
+          static_cast<float*>(pool), slot_idx, q, k, v, gates, y, B, H, G, hpg, T, cus,
+          max_extra);
       break;
     case BRAID_F16:
       gdn_prefill_planned_kernel<F16, Gates><<<grid, block, 0, stream>>>(
-          static_cast<uint16_t*>(pool), slot_idx, q, k, v, gates, y, B, H, G, hpg, T, max_wgs);
+          static_cast<uint16_t*>(pool), slot_idx, q, k, v, gates, y, B, H, G, hpg, T, cus,
+          max_extra);
       break;
     default:
       gdn_prefill_planned_kernel<BF16, Gates><<<grid, block, 0, stream>>>(
-          static_cast<uint16_t*>(pool), slot_idx, q, k, v, gates, y, B, H, G, hpg, T, max_wgs);
+          static_cast<uint16_t*>(pool), slot_idx, q, k, v, gates, y, B, H, G, hpg, T, cus,
+          max_extra);
       break;
   }
 }
