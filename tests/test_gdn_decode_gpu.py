@@ -289,18 +289,20 @@ def test_state_narrowing_rounds_to_nearest_even_exactly(kern, dt):
             "rounded differently from round-to-nearest-even")
 
 
+@pytest.mark.parametrize("H,G", [(32, 16), (12, 4)], ids=["H32", "H12-tiles-not-mult-8"])
 @pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16, torch.float32],
                          ids=["f16-pool", "bf16-pool", "f32-pool"])
-def test_launch_shapes_give_identical_bits(kern, dt, monkeypatch):
+def test_launch_shapes_give_identical_bits(kern, dt, H, G, monkeypatch):
     """A launch of at least 12 tiles per CU walks XCD-contiguous tile ranges
     and, on a 16-bit pool, keeps three workgroups resident per CU. Each tile is
     still one workgroup's work, so every launch shape (forced through the
     override variables) must leave the same pool and y bits; the default one is
-    also checked against the oracle on a sample of rows."""
-    H, G = 32, 16
+    also checked against the oracle on a sample of rows. With H = 12 the tile
+    count is not a multiple of 8, so the default large launch keeps dispatch
+    order (and the cap)."""
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     B = max(128, -(-12 * cus // H))
-    B += (-B) % 8
+    B += (-B) % 8 if H % 8 == 0 else (1 - (B * H // 4) % 2)
     slots = torch.randperm(B + 16, generator=torch.Generator().manual_seed(3))[:B]
     slots = slots.to(torch.int32).to(DEV)
     inp = decode_inputs(B, H=H, G=G, seed=21)
@@ -326,6 +328,8 @@ def test_launch_shapes_give_identical_bits(kern, dt, monkeypatch):
         assert torch.equal(y, y0), label
     rows = [0, B // 2, B - 1]
     sub = slots[rows].cpu().numpy()
+    if H % 8:
+        assert (B * H) % 8 != 0
     ref_pool = to_np_pool(base)
     alpha, beta = torch_gates(a_raw, b_raw, A, dt_bias)
     n = {k: v[rows].cpu().numpy() for k, v in inp.items()}
