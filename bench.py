@@ -454,7 +454,7 @@ def measure_paths(torch, kern):
         ry = torch.randn(ntok, H, D, generator=g, device=dev)
         rz = torch.randn(ntok, H * D, generator=g, device=dev).to(torch.bfloat16)
         t = graph_time(torch, lambda: kern.gated_rmsnorm(ry, rz, gamma, 1e-6), reps=5,
-                       inner=20 if ntok == 64 else 1)
+                       inner=20 if ntok == 64 else 4)
         rbytes = ntok * H * D * READOUT_BYTES_PER_ELEM
         out[label] = {"tokens": ntok, "us": round(t * 1e6, 2),
                       "gbs": round(rbytes / t / 1e9, 1),
