@@ -115,3 +115,29 @@ def test_argument_checks(kern):
         kern.gated_rmsnorm(y[:2], z, gamma, EPS)
     with pytest.raises(RuntimeError, match="fp32 or z's dtype"):
         kern.gated_rmsnorm(y.half(), z, gamma, EPS)
+
+
+def test_silu_gate_is_torchs_spelling_bit_for_bit(kern):
+    """With fp32 activations, y = 1, gamma = 1 and eps = 0 the norm is exactly
+    1, so core = silu(z) as the kernel computes it: z / (1 + exp(-z)) with
+    an IEEE division (braid/model/norm.py:67-71 through F.silu). Every finite
+    bf16 value as z, 4M random fp32 bit patterns and wide normals must equal
+    torch's spelling on the same device bit for bit (NaN for NaN)."""
+    every = torch.arange(0, 1 << 16, device=DEV, dtype=torch.int32).to(torch.int16)
+    every = every.view(torch.bfloat16).float()
+    every = every[torch.isfinite(every)]
+    g = gen(41)
+    bits = torch.randint(-2 ** 31, 2 ** 31 - 1, (1 << 22,), generator=g, device=DEV,
+                         dtype=torch.int32).view(torch.float32)
+    z = torch.cat([every, bits[torch.isfinite(bits)],
+                   torch.randn(1 << 20, generator=g, device=DEV) * 30])
+    n = z.numel() - z.numel() % 128
+    z = z[:n].contiguous()
+    units = n // 128
+    core = kern.gated_rmsnorm(torch.ones(units, 1, 128, device=DEV), z.view(units, 128),
+                              torch.ones(128, device=DEV), 0.0, quantize=False)
+    core = (core[0] if isinstance(core, (tuple, list)) else core).reshape(-1)
+    ref = z / (1 + torch.exp(-z))
+    same = (core.view(torch.int32) == ref.view(torch.int32)) | (core.isnan() & ref.isnan())
+    bad = (~same).nonzero().flatten()[:5]
+    assert bad.numel() == 0, (z[bad].tolist(), core[bad].tolist(), ref[bad].tolist())
