@@ -279,3 +279,30 @@ def test_both_scan_layouts_are_decode_bit_for_bit(kern, monkeypatch, dt, cols):
     torch.cuda.synchronize()
     same = (pc == ps) | (pc.isnan() & ps.isnan())
     assert bool(same.all()), f"states differ by {(pc.float() - ps.float()).abs().max().item():.3e}"
+
+
+def test_a_skewed_ragged_batch_is_decode_bit_for_bit(kern):
+    """One long row among short ones: the default launch plans the long row's
+    tiles in the quarter layout (its chain, not the total work, bounds the
+    batch) and the rest whole. Outputs and states must equal decode applied
+    token by token, bit for bit, with zeros at the pad outputs."""
+    lens_l = [256] + [32] * 15
+    B, T, H, G = len(lens_l), max(lens_l), 32, 16
+    inp = prefill_inputs(B, T, H=H, G=G, seed=31)
+    a, b, A, dtb = raw_gates((B, T, H), H, torch.bfloat16, seed=32)
+    lens = torch.tensor(lens_l, dtype=torch.int32, device=DEV)
+    slots = torch.arange(3, B + 3, dtype=torch.int32, device=DEV)
+    pc = pool(B + 4, H=H, dtype=torch.float16)
+    ps = pc.clone()
+    yc = torch.empty(B, T, H, 128, device=DEV)
+    kern.gdn_prefill_raw(pc, slots, inp["q"], inp["k"], inp["v"], a, b, A, dtb, yc, lens)
+    for t in range(T):
+        live = (t < lens).nonzero().flatten()
+        yt = torch.empty(live.numel(), H, 128, device=DEV)
+        kern.gdn_decode_raw(ps, slots[live].contiguous(), inp["q"][live, t].contiguous(),
+                            inp["k"][live, t].contiguous(), inp["v"][live, t].contiguous(),
+                            a[live, t].contiguous(), b[live, t].contiguous(), A, dtb, yt)
+        assert torch.equal(yc[live, t], yt), f"token {t}: outputs differ"
+    assert bool((yc[1:, 32:] == 0).all()), "pad outputs are not 0"
+    torch.cuda.synchronize()
+    assert torch.equal(pc.view(torch.int16), ps.view(torch.int16))
