@@ -363,11 +363,13 @@ __device__ __forceinline__ void read_token_quarter(const StageLds& st, int j, in
   }
 }
 
-// The live tokens of one tile, with the state resident in registers. Scan
-// layout (ScanMap): four waves; a lane holds the 32 rows of its row block for
-// CPL columns; the column sums finish in-lane and over the four row blocks
-// with permlane swaps, by the decode's summation tree, so the bits are the
-// decode's and no token needs a workgroup barrier. Tokens run in stages of
+// The live tokens of one tile (or of its workgroup's share of the columns),
+// with the state resident in registers. Scan layouts (ScanLayoutOf<Layout>):
+// four waves; a lane holds the 32 rows of its row block for CPL columns
+// (ScanMap), or 16 of them for one column (ScanMapQuarter); the column sums
+// finish in-lane and over the row groups and blocks with DPP / permlane swaps,
+// by the decode's summation tree, so the bits are the decode's and no token
+// needs a workgroup barrier. kTokenPairs runs two tokens per loop iteration. Tokens run in stages of
 // kStage: their inputs are loaded a stage ahead (StageRegs) and staged in LDS
 // (StageLds) between stages, so the serial loop carries only the recurrence
 // and the output stores.
@@ -500,8 +502,9 @@ __device__ __forceinline__ void prefill_tile(typename Storage<Tag>::T* __restric
   }
 }
 
-// One tile (CPL = 2) or one half tile (CPL = 1, kParts = 2) per workgroup:
-// blockIdx.x = (b * H + h) * kParts + part.
+// One tile (layout 2), a half tile (layout 1, kParts = 2) or a quarter tile
+// (layout 4, kParts = 4) per workgroup: blockIdx.x = (b * H + h) * kParts +
+// part. Layouts 1 and 4 run token pairs.
 template <class Tag, class Gates, int Layout>
 __global__ void __launch_bounds__(64 * ScanLayoutOf<Layout>::type::kWaves)
 gdn_prefill_kernel(typename Storage<Tag>::T* __restrict__ pool,
