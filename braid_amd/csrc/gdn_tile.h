@@ -24,8 +24,9 @@
 //      (w0 + w1) + (w2 + w3), evaluated the same way by every lane that needs
 //      the total.
 //
-// Prefill layout (ScanMap: 2 columns per lane, or 1 for small launches, whose
-// tiles are then split over two workgroups): the same rows, chains and tree.
+// Prefill layouts (ScanMap: 2 columns per lane, or 1 for small launches, whose
+// tiles are then split over two workgroups; ScanMapQuarter: 1 column and 16
+// rows per lane, a tile over four workgroups): the same rows, chains and tree.
 // A column's arithmetic does not depend on which lane holds it, so the results
 // are the decode layout's bits.
 //
