@@ -759,8 +759,11 @@ __device__ __forceinline__ void scan_token(Row<Tag, CPL> (&S)[kRowGroups][kRowsP
     for (int i = 0; i < kRowsPerLane; ++i) {
       const int r = rg + kRowGroups * i;
       if constexpr (CPL == 1) {
-        const float n0 = fmaf(alpha, S[rg][i].get(0), kh[r] * delta[0]);
-        S[rg][i].set1(kOpaqueNarrow ? opaque(n0) : n0);
+        // Both uses of the new value take the barrier's output, so it costs
+        // no register copy.
+        float n0 = fmaf(alpha, S[rg][i].get(0), kh[r] * delta[0]);
+        if constexpr (kOpaqueNarrow) n0 = opaque(n0);
+        S[rg][i].set1(n0);
         ch[rg][0] = fmaf(n0, qh[r], ch[rg][0]);
       } else {
 #pragma unroll
@@ -802,8 +805,9 @@ __device__ __forceinline__ void scan_token_quarter(Row<Tag, 1> (&S)[2][kRowsPerL
     ch[g] = 0.f;
 #pragma unroll
     for (int i = 0; i < kRowsPerLane; ++i) {
-      const float n0 = fmaf(alpha, S[g][i].get(0), kh[g][i] * delta);
-      S[g][i].set1(kOpaqueNarrow ? opaque(n0) : n0);
+      float n0 = fmaf(alpha, S[g][i].get(0), kh[g][i] * delta);
+      if constexpr (kOpaqueNarrow) n0 = opaque(n0);
+      S[g][i].set1(n0);
       ch[g] = fmaf(n0, qh[g][i], ch[g]);
     }
   }
