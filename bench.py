@@ -44,6 +44,9 @@ BASELINE shapes, each captured in a hipGraph and timed with events:
   mixer_step        config 3: 24 GDN layers of quant -> conv -> gated decode at
                     B=64, one fp16 pool and conv pool per layer
   mixer_step_fused  the same step with conv + decode fused in one launch
+  prefill_one_row_512, prefill_skewed_1x1024_15x128
+                    small prefill batches: one long row; one long row among
+                    short ones
   mixed_tick        config 4: 4 x 256-token prefill + 96 decode rows on one
                     192-slot fp16 pool; eager and graph-replayed per bucket
 
@@ -415,6 +418,10 @@ def measure_paths(torch, kern):
 
     lens = torch.randint(64, 1025, (8,), generator=torch.Generator().manual_seed(2)).tolist()
     out["prefill_config2"] = prefill_case(lens)
+    # the small-batch regime: one 512-token row (quarter layout, four workgroups
+    # per tile) and one 1024-token row among 15 of 128 (the plan runs it quarter)
+    out["prefill_one_row_512"] = prefill_case([512])
+    out["prefill_skewed_1x1024_15x128"] = prefill_case([1024] + [128] * 15)
 
     # config 2's causal conv prefill: 8 ragged rows, C=8192, K=4, bf16 in, fp32 out
     Cc, Tm = 2 * G * D + H * D, max(lens)
