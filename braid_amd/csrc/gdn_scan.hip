@@ -363,6 +363,67 @@ __device__ __forceinline__ void read_token_quarter(const StageLds& st, int j, in
   }
 }
 
+template <class Tag, int CPL, int kLRG>
+struct ScanState;
+
+// One token of a ScanMap layout (one or two columns per lane) on its state.
+template <class Tag, int CPL, bool kOpaqueNarrow = false>
+__device__ __forceinline__ void scan_token_any(ScanState<Tag, CPL, kRowGroups>& S,
+                                               const TokenIn<CPL>& in, float (&y)[CPL]) {
+  if constexpr (CPL == 1)
+    scan_token_pairs<Tag, kOpaqueNarrow>(S.p, in.kh, in.qh, in.v[0], in.alpha, in.beta, y[0]);
+  else
+    scan_token<Tag, CPL, kOpaqueNarrow>(S.s, in.kh, in.qh, in.v, in.alpha, in.beta, y);
+}
+
+// A lane's state in a scan layout: a Row<Tag, CPL> per (row group, i), or,
+// with one column per lane, row pairs (RowPair1) over row groups 2p and 2p + 1
+// so that one packed conversion narrows two elements.
+template <class Tag, int CPL, int kLRG>
+struct ScanState {
+  Row<Tag, CPL> s[kLRG][kRowsPerLane];
+  template <class LM, class ST>
+  __device__ __forceinline__ void load(const LM& L, const ST* tile) {
+#pragma unroll
+    for (int rg = 0; rg < kLRG; ++rg) {
+#pragma unroll
+      for (int i = 0; i < kRowsPerLane; ++i) s[rg][i].load_nt(tile + (size_t)L.row(rg, i) * kHD);
+    }
+  }
+  template <class LM, class ST>
+  __device__ __forceinline__ void store(const LM& L, ST* tile) const {
+#pragma unroll
+    for (int rg = 0; rg < kLRG; ++rg) {
+#pragma unroll
+      for (int i = 0; i < kRowsPerLane; ++i) s[rg][i].store_nt(tile + (size_t)L.row(rg, i) * kHD);
+    }
+  }
+};
+template <class Tag, int kLRG>
+struct ScanState<Tag, 1, kLRG> {
+  RowPair1<Tag> p[kLRG / 2][kRowsPerLane];
+  template <class LM, class ST>
+  __device__ __forceinline__ void load(const LM& L, const ST* tile) {
+#pragma unroll
+    for (int q = 0; q < kLRG / 2; ++q) {
+#pragma unroll
+      for (int i = 0; i < kRowsPerLane; ++i)
+        p[q][i].load_nt(tile + (size_t)L.row(2 * q, i) * kHD,
+                        tile + (size_t)L.row(2 * q + 1, i) * kHD);
+    }
+  }
+  template <class LM, class ST>
+  __device__ __forceinline__ void store(const LM& L, ST* tile) const {
+#pragma unroll
+    for (int q = 0; q < kLRG / 2; ++q) {
+#pragma unroll
+      for (int i = 0; i < kRowsPerLane; ++i)
+        p[q][i].store_nt(tile + (size_t)L.row(2 * q, i) * kHD,
+                         tile + (size_t)L.row(2 * q + 1, i) * kHD);
+    }
+  }
+};
+
 // The live tokens of one tile (or of its workgroup's share of the columns),
 // with the state resident in registers. Scan layouts (ScanLayoutOf<Layout>):
 // four waves; a lane holds the 32 rows of its row block for CPL columns
@@ -398,12 +459,8 @@ __device__ __forceinline__ void prefill_tile(typename Storage<Tag>::T* __restric
   const int slot = slot_idx[b];
   ST* tile = pool + ((size_t)slot * H + h) * (kSS * kHD) + L.col0;
 
-  Row<Tag, CPL> S[kLRG][kRowsPerLane];
-#pragma unroll
-  for (int rg = 0; rg < kLRG; ++rg) {
-#pragma unroll
-    for (int i = 0; i < kRowsPerLane; ++i) S[rg][i].load_nt(tile + (size_t)L.row(rg, i) * kHD);
-  }
+  ScanState<Tag, CPL, kLRG> S;
+  S.load(L, tile);
 
   constexpr int kW = LM::kWaves;
   // The lane's first row: its row block's (and, in the quarter layout, its
@@ -433,8 +490,10 @@ __device__ __forceinline__ void prefill_tile(typename Storage<Tag>::T* __restric
           read_token_quarter(st, j, r0, L.col0, in0);
           read_token_quarter(st, j + 1, r0, L.col0, in1);
           float y0[1], y1[1];
-          scan_token_quarter<Tag, true>(S, in0.kh, in0.qh, in0.v, in0.alpha, in0.beta, y0[0]);
-          scan_token_quarter<Tag, true>(S, in1.kh, in1.qh, in1.v, in1.alpha, in1.beta, y1[0]);
+          scan_token_quarter<Tag, true>(S.p[0], in0.kh, in0.qh, in0.v, in0.alpha, in0.beta,
+                                        y0[0]);
+          scan_token_quarter<Tag, true>(S.p[0], in1.kh, in1.qh, in1.v, in1.alpha, in1.beta,
+                                        y1[0]);
           if (L.stores_y()) {
             storeN<1>(yt + j * y_tok, y0);
             storeN<1>(yt + (j + 1) * y_tok, y1);
@@ -445,7 +504,7 @@ __device__ __forceinline__ void prefill_tile(typename Storage<Tag>::T* __restric
         TokenInQ in;
         read_token_quarter(st, j, r0, L.col0, in);
         float yy[1];
-        scan_token_quarter<Tag>(S, in.kh, in.qh, in.v, in.alpha, in.beta, yy[0]);
+        scan_token_quarter<Tag>(S.p[0], in.kh, in.qh, in.v, in.alpha, in.beta, yy[0]);
         if (L.stores_y()) storeN<1>(yt + j * y_tok, yy);
       }
     } else if constexpr (kTokenPairs) {
@@ -464,8 +523,8 @@ __device__ __forceinline__ void prefill_tile(typename Storage<Tag>::T* __restric
         read_token<CPL>(st, j, r0, L.col0, in0);
         read_token<CPL>(st, j + 1, r0, L.col0, in1);
         float y0[CPL], y1[CPL];
-        scan_token<Tag, CPL, true>(S, in0.kh, in0.qh, in0.v, in0.alpha, in0.beta, y0);
-        scan_token<Tag, CPL, true>(S, in1.kh, in1.qh, in1.v, in1.alpha, in1.beta, y1);
+        scan_token_any<Tag, CPL, true>(S, in0, y0);
+        scan_token_any<Tag, CPL, true>(S, in1, y1);
         if (L.stores_y()) {
           storeN<CPL>(yt + j * y_tok, y0);
           storeN<CPL>(yt + (j + 1) * y_tok, y1);
@@ -477,18 +536,14 @@ __device__ __forceinline__ void prefill_tile(typename Storage<Tag>::T* __restric
         TokenIn<CPL> in;
         read_token<CPL>(st, j, r0, L.col0, in);
         float yy[CPL];
-        scan_token<Tag, CPL>(S, in.kh, in.qh, in.v, in.alpha, in.beta, yy);
+        scan_token_any<Tag, CPL>(S, in, yy);
         if (L.stores_y()) storeN<CPL>(yt + j * y_tok, yy);
       }
     }
     __syncthreads();
   }
 
-#pragma unroll
-  for (int rg = 0; rg < kLRG; ++rg) {
-#pragma unroll
-    for (int i = 0; i < kRowsPerLane; ++i) S[rg][i].store_nt(tile + (size_t)L.row(rg, i) * kHD);
-  }
+  S.store(L, tile);
 
   // Zeros at the pad positions, the workgroup's columns, 16 bytes per thread.
   constexpr int kCols = LM::kWaves * LM::kColsPerWave;  // this workgroup's columns

@@ -240,6 +240,51 @@ struct Row<BF16, 1> : RowHalf1 {
   __device__ __forceinline__ void set1(float x) { raw = pack_bf16x2(x, 0.f) & 0xffffu; }
 };
 
+// Two rows' elements of one column (the one-column prefill layouts): row a in
+// bits 0..15 of one register, row b in bits 16..31, so one packed conversion
+// narrows both (the mixed-precision fma reads either half directly). Each
+// element is rounded on its own, as the single-element rows round it.
+template <class Tag>
+struct RowPair1;
+template <>
+struct RowPair1<F32> {
+  float d0, d1;
+  __device__ __forceinline__ void load_nt(const float* a, const float* b) {
+    d0 = __builtin_nontemporal_load(a);
+    d1 = __builtin_nontemporal_load(b);
+  }
+  __device__ __forceinline__ void store_nt(float* a, float* b) const {
+    __builtin_nontemporal_store(d0, a);
+    __builtin_nontemporal_store(d1, b);
+  }
+  __device__ __forceinline__ float get(int h) const { return h ? d1 : d0; }
+  __device__ __forceinline__ void set(float lo, float hi) {
+    d0 = lo;
+    d1 = hi;
+  }
+};
+struct RowHalfPair {
+  uint32_t raw;
+  __device__ __forceinline__ void load_nt(const uint16_t* a, const uint16_t* b) {
+    raw = (uint32_t)__builtin_nontemporal_load(a) | ((uint32_t)__builtin_nontemporal_load(b) << 16);
+  }
+  __device__ __forceinline__ void store_nt(uint16_t* a, uint16_t* b) const {
+    __builtin_nontemporal_store((uint16_t)raw, a);
+    __builtin_nontemporal_store((uint16_t)(raw >> 16), b);
+  }
+  __device__ __forceinline__ uint32_t bits(int h) const { return h ? raw >> 16 : raw & 0xffffu; }
+};
+template <>
+struct RowPair1<F16> : RowHalfPair {
+  __device__ __forceinline__ float get(int h) const { return f16_widen(bits(h)); }
+  __device__ __forceinline__ void set(float lo, float hi) { raw = pack_f16x2(lo, hi); }
+};
+template <>
+struct RowPair1<BF16> : RowHalfPair {
+  __device__ __forceinline__ float get(int h) const { return bf16_widen(bits(h)); }
+  __device__ __forceinline__ void set(float lo, float hi) { raw = pack_bf16x2(lo, hi); }
+};
+
 // ---------------------------------------------------------------------------
 // Cross-lane sums. Butterflies over lane-index bits: partners add the same two
 // operands (a + b == b + a), so after every stage all lanes of a group hold
@@ -782,34 +827,75 @@ __device__ __forceinline__ void scan_token(Row<Tag, CPL> (&S)[kRowGroups][kRowsP
     y[c] = scan_column_sum(ch[0][c], ch[1][c], ch[2][c], ch[3][c]) * kYScale;
 }
 
+// The one-column layout's token over row pairs: P[p][i] holds rows of row
+// groups 2p (low half) and 2p + 1 (high half), i.e. rows w * 32 + rg + 4 i.
+// Each element's operations and each chain's order are scan_token's.
+template <class Tag, bool kOpaqueNarrow = false>
+__device__ __forceinline__ void scan_token_pairs(RowPair1<Tag> (&P)[2][kRowsPerLane],
+                                                 const float (&kh)[kRowsPerWave],
+                                                 const float (&qh)[kRowsPerWave], float v,
+                                                 float alpha, float beta, float& y) {
+  float ch[kRowGroups];
+#pragma unroll
+  for (int rg = 0; rg < kRowGroups; ++rg) {
+    ch[rg] = P[rg >> 1][0].get(rg & 1) * kh[rg];
+#pragma unroll
+    for (int i = 1; i < kRowsPerLane; ++i)
+      ch[rg] = fmaf(P[rg >> 1][i].get(rg & 1), kh[rg + kRowGroups * i], ch[rg]);
+  }
+  const float kv = scan_column_sum(ch[0], ch[1], ch[2], ch[3]);
+  const float delta = (v - alpha * kv) * beta;
+#pragma unroll
+  for (int rg = 0; rg < kRowGroups; ++rg) ch[rg] = 0.f;
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+#pragma unroll
+    for (int i = 0; i < kRowsPerLane; ++i) {
+      float n[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        n[h] = fmaf(alpha, P[p][i].get(h), kh[2 * p + h + kRowGroups * i] * delta);
+        if constexpr (kOpaqueNarrow) n[h] = opaque(n[h]);
+      }
+      P[p][i].set(n[0], n[1]);
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        ch[2 * p + h] = fmaf(n[h], qh[2 * p + h + kRowGroups * i], ch[2 * p + h]);
+    }
+  }
+  y = scan_column_sum(ch[0], ch[1], ch[2], ch[3]) * kYScale;
+}
+
 // One token of the quarter layout on this lane's 16 rows x 1 column: S[rgl][i]
 // is row w * 32 + 2 rgh + rgl + 4 i, kh / qh hold the same rows. Each
 // element's operations are scan_token's (and so the decode's), in the same
 // order; the column totals follow the layout's tree.
 template <class Tag, bool kOpaqueNarrow = false>
-__device__ __forceinline__ void scan_token_quarter(Row<Tag, 1> (&S)[2][kRowsPerLane],
+__device__ __forceinline__ void scan_token_quarter(RowPair1<Tag> (&P)[kRowsPerLane],
                                                    const float (&kh)[2][kRowsPerLane],
                                                    const float (&qh)[2][kRowsPerLane], float v,
                                                    float alpha, float beta, float& y) {
   float ch[2];
 #pragma unroll
   for (int g = 0; g < 2; ++g) {
-    ch[g] = S[g][0].get(0) * kh[g][0];
+    ch[g] = P[0].get(g) * kh[g][0];
 #pragma unroll
-    for (int i = 1; i < kRowsPerLane; ++i) ch[g] = fmaf(S[g][i].get(0), kh[g][i], ch[g]);
+    for (int i = 1; i < kRowsPerLane; ++i) ch[g] = fmaf(P[i].get(g), kh[g][i], ch[g]);
   }
   const float kv = add_xor32(add_xor16(add_xor8(ch[0] + ch[1])));
   const float delta = (v - alpha * kv) * beta;
+  ch[0] = ch[1] = 0.f;
 #pragma unroll
-  for (int g = 0; g < 2; ++g) {
-    ch[g] = 0.f;
+  for (int i = 0; i < kRowsPerLane; ++i) {
+    float n[2];
 #pragma unroll
-    for (int i = 0; i < kRowsPerLane; ++i) {
-      float n0 = fmaf(alpha, S[g][i].get(0), kh[g][i] * delta);
-      if constexpr (kOpaqueNarrow) n0 = opaque(n0);
-      S[g][i].set1(n0);
-      ch[g] = fmaf(n0, qh[g][i], ch[g]);
+    for (int g = 0; g < 2; ++g) {
+      n[g] = fmaf(alpha, P[i].get(g), kh[g][i] * delta);
+      if constexpr (kOpaqueNarrow) n[g] = opaque(n[g]);
     }
+    P[i].set(n[0], n[1]);
+#pragma unroll
+    for (int g = 0; g < 2; ++g) ch[g] = fmaf(n[g], qh[g][i], ch[g]);
   }
   y = add_xor32(add_xor16(add_xor8(ch[0] + ch[1]))) * kYScale;
 }
