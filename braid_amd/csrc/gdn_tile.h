@@ -217,6 +217,15 @@ __device__ __forceinline__ float opaque(float x) {
   return x;
 }
 
+// The first term of a kv chain, S * kh, as fma(S, kh, -0): equal to the
+// rounded product for every input (adding -0 changes no value and keeps a -0
+// product), and one mixed-precision fma on a 16-bit S instead of a widening
+// and a multiply. The -0 goes through opaque() so the fma is not folded back
+// into the multiply.
+__device__ __forceinline__ float first_term(float s, float kh, float neg_zero) {
+  return fmaf(s, kh, neg_zero);
+}
+
 struct RowHalf1 {
   uint32_t raw;  // the element in bits 0..15
   __device__ __forceinline__ void load_nt(const uint16_t* p) {
@@ -780,10 +789,11 @@ __device__ __forceinline__ void scan_token(Row<Tag, CPL> (&S)[kRowGroups][kRowsP
                                            const float (&v)[CPL], float alpha, float beta,
                                            float (&y)[CPL]) {
   float ch[kRowGroups][CPL];
+  const float nz = opaque(-0.0f);
 #pragma unroll
   for (int rg = 0; rg < kRowGroups; ++rg) {
 #pragma unroll
-    for (int c = 0; c < CPL; ++c) ch[rg][c] = S[rg][0].get(c) * kh[rg];
+    for (int c = 0; c < CPL; ++c) ch[rg][c] = first_term(S[rg][0].get(c), kh[rg], nz);
 #pragma unroll
     for (int i = 1; i < kRowsPerLane; ++i) {
 #pragma unroll
@@ -836,9 +846,10 @@ __device__ __forceinline__ void scan_token_pairs(RowPair1<Tag> (&P)[2][kRowsPerL
                                                  const float (&qh)[kRowsPerWave], float v,
                                                  float alpha, float beta, float& y) {
   float ch[kRowGroups];
+  const float nz = opaque(-0.0f);
 #pragma unroll
   for (int rg = 0; rg < kRowGroups; ++rg) {
-    ch[rg] = P[rg >> 1][0].get(rg & 1) * kh[rg];
+    ch[rg] = first_term(P[rg >> 1][0].get(rg & 1), kh[rg], nz);
 #pragma unroll
     for (int i = 1; i < kRowsPerLane; ++i)
       ch[rg] = fmaf(P[rg >> 1][i].get(rg & 1), kh[rg + kRowGroups * i], ch[rg]);
@@ -876,9 +887,10 @@ __device__ __forceinline__ void scan_token_quarter(RowPair1<Tag> (&P)[kRowsPerLa
                                                    const float (&qh)[2][kRowsPerLane], float v,
                                                    float alpha, float beta, float& y) {
   float ch[2];
+  const float nz = opaque(-0.0f);
 #pragma unroll
   for (int g = 0; g < 2; ++g) {
-    ch[g] = P[0].get(g) * kh[g][0];
+    ch[g] = first_term(P[0].get(g), kh[g][0], nz);
 #pragma unroll
     for (int i = 1; i < kRowsPerLane; ++i) ch[g] = fmaf(P[i].get(g), kh[g][i], ch[g]);
   }
