@@ -6,8 +6,11 @@ per head, fp32 recurrence math, in-kernel gates from bf16 raw projections) on
 a 160-slot fp16 state pool addressed through a random permutation of 128
 distinct slots. Synthetic inputs, seeded.
 
-Timing: K steps are captured in one hipGraph and replayed once between two
-synchronisations, timed with events on the stream the kernels run on. The
+Timing: K steps are captured in one hipGraph; the graph is replayed 31 times,
+each replay between two synchronisations and timed alone with events on the
+stream the kernels run on, behind a short GPU busy-wait so that the host has
+queued the replay before the start event fires. `value` and `ms_per_step` are
+the median replay (the reference's measure_graphed, noise_floor.py:52-105). The
 default is COLD: step i runs on pool i % P, with P pools totalling > 1 GiB, so
 neither the L2s nor the 256 MB Infinity Cache hold a state slab when it is
 revisited (a single 160 MiB pool would fit and report above-HBM figures). The
@@ -111,12 +114,35 @@ def make_workload(torch, n_pools, seed=0):
     return pools, slot_maps, inputs, A, dt_bias
 
 
-def time_steps(torch, kern, work, steps, warmup, spread_reps=0):
-    """Capture `steps` decode launches (step i on pool i % P) in one graph,
-    replay it once between synchronisations; returns seconds for all steps.
-    With spread_reps > 0 the graph is then replayed that many more times, each
-    timed alone, and the per-step p10 / p50 / p90 microseconds of those replays
-    are returned too (the timed replay above stays the reported figure)."""
+def _busy(torch):
+    """Keep the GPU busy for ~0.2 ms so that the host has queued the graph
+    replay behind the start event before the GPU reaches it: the timed
+    region then holds the K steps' GPU time, not the host's submission
+    latency of the graph."""
+    torch.cuda._sleep(200_000)
+
+
+def replay_times(torch, graph, reps):
+    """Seconds of each of `reps` replays of `graph`, each bracketed by
+    synchronisations and timed with events on the launch stream."""
+    out = []
+    for _ in range(reps):
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        _busy(torch)
+        a.record()
+        graph.replay()
+        b.record()
+        torch.cuda.synchronize()
+        out.append(a.elapsed_time(b) / 1e3)
+    return out
+
+
+def time_steps(torch, kern, work, steps, warmup, reps=31):
+    """Capture `steps` decode launches (step i on pool i % P) in one graph
+    and replay it `reps` times, each replay timed alone (the reference's
+    measure_graphed, braid/bench/noise_floor.py:52-105). Returns the median
+    seconds per replay and the per-step spread of the replays."""
     pools, slot_maps, inputs, A, dtb = work
     P = len(pools)
 
@@ -135,27 +161,14 @@ def time_steps(torch, kern, work, steps, warmup, spread_reps=0):
             launch(i)
     graph.replay()                       # untimed: first replay uploads the graph
     torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    start.record()
-    graph.replay()
-    end.record()
-    torch.cuda.synchronize()
-    total = start.elapsed_time(end) / 1e3
-    if spread_reps <= 0:
-        return total
-    per_step = []
-    for _ in range(spread_reps):
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
-        graph.replay()
-        b.record()
-        torch.cuda.synchronize()
-        per_step.append(a.elapsed_time(b) * 1e3 / steps)
-    per_step.sort()
-    q = lambda f: round(per_step[min(len(per_step) - 1, int(f * len(per_step)))], 3)
-    return total, {"reps": spread_reps, "steps_per_rep": steps, "p10_us": q(0.1),
-                   "p50_us": q(0.5), "p90_us": q(0.9)}
+    times = replay_times(torch, graph, reps)
+    first = times[0]
+    times.sort()
+    q = lambda f: round(times[min(len(times) - 1, int(f * len(times)))] * 1e6 / steps, 3)
+    median = times[len(times) // 2]
+    return median, {"reps": reps, "steps_per_rep": steps, "p10_us": q(0.1),
+                    "p50_us": q(0.5), "p90_us": q(0.9),
+                    "first_rep_us": round(first * 1e6 / steps, 3)}
 
 
 def copy_bandwidth(torch, nbytes=2 ** 30):
@@ -224,12 +237,8 @@ def stream_ceiling(torch, n_pools, launches=256):
                 launch(i)
         graph.replay()
         torch.cuda.synchronize()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
-        graph.replay()
-        b.record()
-        torch.cuda.synchronize()
-        secs = a.elapsed_time(b) / 1e3 / launches
+        t = sorted(replay_times(torch, graph, 5))
+        secs = t[len(t) // 2] / launches
         out[f"{label}_us"] = round(secs * 1e6, 2)
         out[f"{label}_gbs"] = round(nbytes / secs / 1e9, 1)
     del pools
@@ -318,7 +327,7 @@ ROW_BYTES = 2 * H * D * D * 2 + (2 * G * D + 2 * H * D) * 4 + H * 2 * 2 + 4
 READOUT_BYTES_PER_ELEM = 4 + 2 + 2 + 2 + 1
 
 
-def graph_time(torch, fn, reps=5, inner=1, before_replay=None):
+def graph_time(torch, fn, reps=11, inner=1, before_replay=None):
     """Median seconds per call of `fn`, replayed from a captured graph.
     `before_replay` runs once after capture (e.g. to point padded rows at a
     scratch slot, which eager validation would refuse as a duplicate)."""
@@ -344,15 +353,7 @@ def graph_time(torch, fn, reps=5, inner=1, before_replay=None):
         graph.replay()
         torch.cuda.synchronize()
         n_warm += 1
-    times = []
-    for _ in range(reps):
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
-        graph.replay()
-        b.record()
-        torch.cuda.synchronize()
-        times.append(a.elapsed_time(b) / 1e3 / inner)
-    times.sort()
+    times = sorted(t / inner for t in replay_times(torch, graph, reps))
     return times[len(times) // 2]
 
 
@@ -375,7 +376,7 @@ def measure_paths(torch, kern):
         y = torch.empty(Bp, T, H, D, device=dev)
         sl = torch.tensor(lens, dtype=torch.int32, device=dev)
         t = graph_time(torch, lambda: kern.gdn_prefill_raw(pool, slots, q, k, v, a, b, A, dtb,
-                                                           y, sl), reps=5)
+                                                           y, sl), reps=11)
         tok = sum(lens)
         tf = tok * H * FLOP_PER_TOKEN_HEAD / t / 1e12
         return {"rows": Bp, "max_T": T, "tokens": tok, "ms": round(t * 1e3, 3),
@@ -396,7 +397,7 @@ def measure_paths(torch, kern):
         db = torch.randn(B, H, generator=g, device=dev).to(torch.bfloat16)
         dy = torch.empty(B, H, D, device=dev)
         t = graph_time(torch, lambda: kern.gdn_decode_raw(dpool, dslots, dq, dk, dv, da, db, A,
-                                                          dtb, dy), reps=5, inner=20)
+                                                          dtb, dy), reps=11, inner=20)
         nbytes = STEP_BYTES + B * H * D * D * 2 * (elem - 2)
         out[label] = {"us": round(t * 1e6, 2), "steps_per_s": round(1 / t, 1),
                       "gbs": round(nbytes / t / 1e9, 1),
@@ -409,7 +410,7 @@ def measure_paths(torch, kern):
     dalpha = torch.rand(B, H, generator=g, device=dev) * 0.5 + 0.5
     dbeta = torch.rand(B, H, generator=g, device=dev)
     t = graph_time(torch, lambda: kern.gdn_decode(dpool, dslots, dq, dk, dv, dalpha, dbeta, dy),
-                   reps=5, inner=20)
+                   reps=11, inner=20)
     nbytes = STEP_BYTES + B * H * 4
     out["decode_b128_fp16_precomputed_gates"] = {
         "us": round(t * 1e6, 2), "steps_per_s": round(1 / t, 1),
@@ -432,7 +433,7 @@ def measure_paths(torch, kern):
     cout = torch.empty(8, Tm, Cc, device=dev)
     clens = torch.tensor(lens, dtype=torch.int32, device=dev)
     t = graph_time(torch, lambda: kern.conv1d_prefill(cpool, cslots, cx, cw, None, cout, clens),
-                   reps=5)
+                   reps=11)
     cbytes = 8 * Tm * Cc * (2 + 4) + 2 * 8 * Cc * 4 * 4 + Cc * 4 * 4
     out["conv1d_prefill_config2"] = {"tokens": sum(lens), "padded_T": Tm,
                                      "us": round(t * 1e6, 1),
@@ -451,13 +452,13 @@ def measure_paths(torch, kern):
     xc = torch.randn(64, C, generator=g, device=dev).to(torch.bfloat16)
     co = torch.empty(64, C, device=dev)
     t = graph_time(torch, lambda: kern.conv1d_decode(conv_pool, slots64, xc, w, bias, co),
-                   reps=5, inner=20)
+                   reps=11, inner=20)
     out["conv1d_decode"] = {"shape": "B=64 C=8192 K=4 bf16", "us": round(t * 1e6, 2),
                             "gbs": round(CONV_BYTES_B64 / t / 1e9, 1),
                             "hbm_frac": round(CONV_BYTES_B64 / t / 1e9 / HBM_PEAK_GBS, 4)}
 
     xq = torch.randn(64, 4096, generator=g, device=dev).to(torch.bfloat16)
-    t = graph_time(torch, lambda: kern.quantize_act(xq), reps=5, inner=20)
+    t = graph_time(torch, lambda: kern.quantize_act(xq), reps=11, inner=20)
     out["quantize_act"] = {"shape": "64x4096 bf16", "us": round(t * 1e6, 2),
                            "gbs": round(QUANT_BYTES_64x4096 / t / 1e9, 1)}
 
@@ -467,7 +468,7 @@ def measure_paths(torch, kern):
     for label, ntok in (("readout_quant_b64", 64), ("readout_quant_prefill", sum(lens))):
         ry = torch.randn(ntok, H, D, generator=g, device=dev)
         rz = torch.randn(ntok, H * D, generator=g, device=dev).to(torch.bfloat16)
-        t = graph_time(torch, lambda: kern.gated_rmsnorm(ry, rz, gamma, 1e-6), reps=5,
+        t = graph_time(torch, lambda: kern.gated_rmsnorm(ry, rz, gamma, 1e-6), reps=11,
                        inner=20 if ntok == 64 else 4)
         rbytes = ntok * H * D * READOUT_BYTES_PER_ELEM
         out[label] = {"tokens": ntok, "us": round(t * 1e6, 2),
@@ -482,10 +483,10 @@ def measure_paths(torch, kern):
     xgq, sxg = kern.quantize_act(xg)
     for label, N in (("fp8_gemm_in_proj_b64", 12288), ("fp8_gemm_out_proj_b64", 4096)):
         wq, sw = kern.quantize_act(torch.randn(N, 4096, generator=g, device=dev) * 0.02)
-        t = graph_time(torch, lambda: kern.fp8_matmul(xgq, sxg, wq, sw), reps=5, inner=20)
+        t = graph_time(torch, lambda: kern.fp8_matmul(xgq, sxg, wq, sw), reps=11, inner=20)
         t_ref = graph_time(torch, lambda: torch._scaled_mm(xgq, wq.t(), scale_a=sxg, scale_b=sw,
                                                            out_dtype=torch.bfloat16),
-                           reps=5, inner=20)
+                           reps=11, inner=20)
         gbytes = N * 4096 + 64 * 4096 + 64 * N * 2
         out[label] = {"shape": f"M=64 N={N} K=4096", "us": round(t * 1e6, 2),
                       "gbs": round(gbytes / t / 1e9, 1),
@@ -517,7 +518,7 @@ def measure_paths(torch, kern):
                                 k.unflatten(-1, (G, D)), v.unflatten(-1, (H, D)), ly["a"],
                                 ly["b"], A, dtb, ly["y"])
 
-    t = graph_time(torch, mixer_step, reps=5)
+    t = graph_time(torch, mixer_step, reps=11)
     step_bytes = L * (QUANT_BYTES_64x4096 + CONV_BYTES_B64 + Bm * ROW_BYTES)
 
     def mixer_step_fused():
@@ -526,7 +527,7 @@ def measure_paths(torch, kern):
             kern.gdn_conv_decode_raw(ly["pool"], ly["conv"], slots64, ly["xin"], ly["w"],
                                      ly["bias"], ly["a"], ly["b"], A, dtb, ly["y"], G)
 
-    t_fused = graph_time(torch, mixer_step_fused, reps=5)
+    t_fused = graph_time(torch, mixer_step_fused, reps=11)
     out["mixer_step_fused"] = {"layers": L, "batch": Bm, "us": round(t_fused * 1e6, 1),
                                "gbs": round(step_bytes / t_fused / 1e9, 1),
                                "hbm_frac": round(step_bytes / t_fused / 1e9 / HBM_PEAK_GBS, 4),
@@ -566,17 +567,24 @@ def measure_paths(torch, kern):
             kern.gdn_prefill_raw(pool, pre_slots, pq, pk, pv, pa, pb, A, dtb, py, plen)
             kern.gdn_decode_raw(pool, sl, dq, dk, dv, da, db, A, dtb, dy)
 
-        entry = {"graph_us": round(graph_time(torch, tick_fn, reps=5,
+        entry = {"graph_us": round(graph_time(torch, tick_fn, reps=11,
                                               before_replay=lambda: sl.copy_(padded)) * 1e6, 1)}
-        sl.copy_(torch.arange(bucket, dtype=torch.int32, device=dev))
-        if bucket <= 96:  # eager needs distinct slots (no scratch padding)
+        # eager: the kernels' eager validation wants distinct slots, so the
+        # pad rows of bucket 128 take distinct free slots (100..131; the
+        # prefill rows own 96..99) instead of one scratch slot
+        eager_sl = torch.cat([torch.arange(live, dtype=torch.int32, device=dev),
+                              torch.arange(100, 100 + bucket - live, dtype=torch.int32,
+                                           device=dev)])
+        sl.copy_(eager_sl)
+        tick_fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(5):
             tick_fn()
-            torch.cuda.synchronize()
-            t0 = time.perf_counter()
-            for _ in range(5):
-                tick_fn()
-            torch.cuda.synchronize()
-            entry["eager_us"] = round((time.perf_counter() - t0) / 5 * 1e6, 1)
+        torch.cuda.synchronize()
+        entry["eager_us"] = round((time.perf_counter() - t0) / 5 * 1e6, 1)
+        if bucket > live:
+            entry["eager_pad"] = f"{bucket - live} pad rows on distinct free slots"
         tick[str(bucket)] = entry
     tick_bytes = 96 * ROW_BYTES + 4 * 2 * H * D * D * 2 + 4 * 256 * (
         (2 * G * D + 2 * H * D) * 4 + H * 2 * 2)
@@ -599,9 +607,9 @@ def main():
     kern = load_gdn()
     n_cold = max(2, math.ceil(COLD_BYTES / (SLOTS * H * D * D * 2)))
     work = make_workload(torch, n_cold)
-    t_cold, spread = time_steps(torch, kern, work, args.steps, args.warmup, spread_reps=30)
+    t_cold, spread = time_steps(torch, kern, work, args.steps, args.warmup)
     hot_work = tuple([x[:1] for x in work[:3]] + list(work[3:]))
-    t_hot = time_steps(torch, kern, hot_work, args.steps, args.warmup)
+    t_hot, _ = time_steps(torch, kern, hot_work, args.steps, args.warmup, reps=11)
     del work, hot_work
     torch.cuda.empty_cache()
     copy_gbs = copy_bandwidth(torch)
@@ -635,7 +643,8 @@ def main():
                      "traffic": traffic},
         "achieved_gbs": round(achieved, 1),
         "hbm_frac": round(achieved / HBM_PEAK_GBS, 4),
-        # 30 further replays of the same graph, each timed alone: per-step spread
+        # value and ms_per_step are the median of these replays (each of all
+        # K steps, timed alone); first_rep_us is the first timed replay alone
         "spread_us_per_step": spread,
         "hot_steps_per_s": round(args.steps / t_hot, 2),
         "hot_achieved_gbs": round(STEP_BYTES / (t_hot / args.steps) / 1e9, 1),

@@ -1,12 +1,34 @@
 // Error reporting and slot validation for the C ABI (host code only).
 #include "capi_common.h"
 
+#include <atomic>
+#include <cstdlib>
 #include <vector>
 
 namespace braid {
 
 namespace {
 thread_local std::string g_last_error;
+
+constexpr int kKnobs = 4;
+const char* const kKnobEnv[kKnobs] = {"BRAID_DECODE_XCD_REMAP", "BRAID_DECODE_WGS_PER_CU",
+                                      "BRAID_PREFILL_COLS", "BRAID_DECODE_PARTS"};
+
+// Read once, at library load (static initialisation), not per launch.
+struct Knobs {
+  std::atomic<int> v[kKnobs];
+  Knobs() {
+    for (int i = 0; i < kKnobs; ++i) {
+      const char* e = std::getenv(kKnobEnv[i]);
+      v[i].store(e != nullptr && e[0] != '\0' ? std::atoi(e) : -1, std::memory_order_relaxed);
+    }
+  }
+};
+Knobs g_knobs;
+}  // namespace
+
+int launch_knob(int knob) {
+  return knob >= 0 && knob < kKnobs ? g_knobs.v[knob].load(std::memory_order_relaxed) : -1;
 }
 
 int fail(int code, const std::string& msg) {
@@ -70,5 +92,14 @@ extern "C" {
 int braid_abi_version(void) { return 1; }
 
 const char* braid_last_error(void) { return braid::g_last_error.c_str(); }
+
+int braid_set_launch_override(int knob, int value) {
+  if (knob < 0 || knob >= braid::kKnobs)
+    return braid::fail(BRAID_EINVAL, "unknown launch knob " + std::to_string(knob));
+  braid::g_knobs.v[knob].store(value < 0 ? -1 : value, std::memory_order_relaxed);
+  return braid::ok();
+}
+
+int braid_get_launch_override(int knob) { return braid::launch_knob(knob); }
 
 }  // extern "C"

@@ -744,7 +744,9 @@ int launch_decode(void* pool, int pool_dtype, const int32_t* slot_idx, int B, in
   const dim3 grid((unsigned)B * (unsigned)H), block(tile_threads(kDecodeCols));
   const int hpg = H / G;
   const StreamShape shape =
-      stream_shape((long)B * H, device_cus(), pool_dtype != BRAID_F32, sizeof(TileLds));
+      stream_shape((long)B * H, device_cus(), pool_dtype != BRAID_F32, sizeof(TileLds),
+                   launch_knob(BRAID_KNOB_DECODE_XCD_REMAP),
+                   launch_knob(BRAID_KNOB_DECODE_WGS_PER_CU));
   const size_t lds_pad = shape.lds_pad;
   const int xr = shape.xcd_contiguous;
   switch (pool_dtype) {
@@ -775,13 +777,12 @@ int launch_decode(void* pool, int pool_dtype, const int32_t* slot_idx, int B, in
 // Measured (MI355X, 256 CUs): one 512-token row 0.315 ms in layout 1, 0.225 ms
 // in layout 4; rows (300, 700) 0.425 -> 0.301 ms; config 4's 128 tiles, where
 // layout 4 would put two workgroups on every CU, 0.183 in layout 1 against
-// 0.190 ms. BRAID_PREFILL_COLS (1, 2, 4, or 0 for planned when seq_lens is
-// given) overrides the choice.
+// 0.190 ms. The PREFILL_LAYOUT launch knob (1, 2, 4, or 0 for planned when
+// seq_lens is given) overrides the choice.
 int prefill_layout(int n_tiles, int B, bool ragged, int cus) {
-  const char* env = std::getenv("BRAID_PREFILL_COLS");
-  if (env != nullptr && (std::atoi(env) == 1 || std::atoi(env) == 2 || std::atoi(env) == 4))
-    return std::atoi(env);
-  if (env != nullptr && env[0] == '0' && ragged && B <= kMaxPlanRows) return 0;
+  const int forced = launch_knob(BRAID_KNOB_PREFILL_LAYOUT);
+  if (forced == 1 || forced == 2 || forced == 4) return forced;
+  if (forced == 0 && ragged && B <= kMaxPlanRows) return 0;
   if (cus > 0 && 4 * n_tiles <= cus) return 4;
   if (cus > 0 && 2 * n_tiles <= cus) return 1;
   return ragged && B <= kMaxPlanRows && cus > 0 && n_tiles <= 4 * cus ? 0 : 2;

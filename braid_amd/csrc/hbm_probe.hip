@@ -83,7 +83,11 @@ int braid_probe_stream(int kind, void* base, int64_t n_tiles, const int32_t* til
   if (hipGetDevice(&dev) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
     cus = 0;
-  const braid::StreamShape sh = braid::stream_shape(n_tiles, cus, true, 4104);
+  // The decode's overrides, read once from the environment as the kernel
+  // library reads them.
+  static const int remap_env = braid::env_int("BRAID_DECODE_XCD_REMAP");
+  static const int cap_env = braid::env_int("BRAID_DECODE_WGS_PER_CU");
+  const braid::StreamShape sh = braid::stream_shape(n_tiles, cus, true, 4104, remap_env, cap_env);
   if (kind == 0)
     probe_rmw<<<grid, block, sh.lds_pad, s>>>(static_cast<char*>(base), tile_idx,
                                               sh.xcd_contiguous);

@@ -18,8 +18,11 @@
 //   with fewer rounds the coarser last round costs more (B = 32: 14.9 ->
 //   16.0 us uncapped vs capped), and fp32 tiles gain nothing.
 //
-// BRAID_DECODE_XCD_REMAP (0 / 1) and BRAID_DECODE_WGS_PER_CU (0: uncapped,
-// N > 0: N) override the choices, for measurement.
+// The caller passes overrides for measurement (-1: no override): remap 0 / 1,
+// cap 0 (uncapped) or N > 0. The kernel library takes them from its launch
+// knobs, which are read from the environment once, when the library loads,
+// and can be set with braid_set_launch_override; a captured graph keeps the
+// launch shape it was captured with.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -42,18 +45,17 @@ struct StreamShape {
   size_t lds_pad;      // dynamic LDS bytes to request
 };
 
-inline int env_override(const char* name) {
+// An integer from the environment, or -1 when the variable is unset.
+inline int env_int(const char* name) {
   const char* e = getenv(name);
   return e ? atoi(e) : -1;
 }
 
 // cus: CUs of the device (0 if unknown: no large-launch choices);
-// narrow: 16-bit tiles; static_lds: the kernel's own LDS bytes.
-inline StreamShape stream_shape(long n_tiles, int cus, bool narrow, size_t static_lds) {
-  // Read per launch (two getenv calls), so a process can change them between
-  // launches.
-  const int remap_env = env_override("BRAID_DECODE_XCD_REMAP");
-  const int cap_env = env_override("BRAID_DECODE_WGS_PER_CU");
+// narrow: 16-bit tiles; static_lds: the kernel's own LDS bytes;
+// remap_env / cap_env: overrides, -1 for none.
+inline StreamShape stream_shape(long n_tiles, int cus, bool narrow, size_t static_lds,
+                                int remap_env = -1, int cap_env = -1) {
   const bool large = cus > 0 && n_tiles >= 12L * cus;
   StreamShape s{0, 0};
   const bool remap = remap_env >= 0 ? remap_env > 0 : large;

@@ -17,7 +17,15 @@ not move the per-tensor FP8 scale of the live rows either.
 
 Under capture the kernels skip their eager slot-map validation (a device to
 host copy is illegal while capturing), which is also what lets several padded
-rows share one scratch slot.
+rows share one scratch slot. A replay therefore trusts the slot buffer, and
+``step`` validates what it copies in (``validate=True``, the default): every
+slot in ``[0, max_slots)``, live slots distinct, and no pad slot equal to a
+live one. An out-of-range slot would make the kernels write outside the pool,
+and a repeated live slot would let two rows race on one state slab; the eager
+entry points reject both, and so does ``step``. The check reads the slots on
+the host (one small device-to-host copy when they live on the GPU, the same
+synchronisation an eager launch pays); ``validate=False`` skips it for
+callers that guarantee the contract themselves.
 """
 from __future__ import annotations
 
@@ -132,17 +140,46 @@ class GraphedDecoder:
         return _Bucket(graph=graph, inputs=inputs, slots=slots, slots_i32=slots_i32,
                        outputs=outputs, size=size)
 
+    def check_slots(self, slots: torch.Tensor, pad_slots: Optional[torch.Tensor],
+                    n_pad: int) -> None:
+        """Raise ValueError unless every live slot lies in ``[0, max_slots)``
+        and is distinct, and the ``n_pad`` pad slots used lie in range and
+        name no live slot. The messages follow the eager entry points'."""
+        n = self.cache.max_slots
+        live = [int(s) for s in slots.reshape(-1).tolist()]
+        pads = [] if n_pad == 0 else [int(s) for s in pad_slots.reshape(-1)[:n_pad].tolist()]
+        if len(pads) < n_pad:
+            raise ValueError(f"pad_slots holds {len(pads)} slots; {n_pad} rows are padding")
+        for i, s in enumerate(live):
+            if not 0 <= s < n:
+                raise ValueError(f"slot_idx[{i}] = {s} is out of range [0, {n})")
+        if len(set(live)) != len(live):
+            dup = next(s for s in live if live.count(s) > 1)
+            raise ValueError(f"slot_idx has duplicate slot {dup}; two live rows sharing one "
+                             f"state slab is silent cross-sequence corruption. Slots must be "
+                             f"distinct.")
+        for i, s in enumerate(pads):
+            if not 0 <= s < n:
+                raise ValueError(f"pad_slots[{i}] = {s} is out of range [0, {n})")
+        clash = set(pads) & set(live)
+        if clash:
+            raise ValueError(f"pad slot {min(clash)} is also a live slot; padded rows would "
+                             f"advance that sequence's state")
+
     def step(self, inputs: Any, slots: torch.Tensor,
-             pad_slots: Optional[torch.Tensor] = None) -> Any:
+             pad_slots: Optional[torch.Tensor] = None, validate: bool = True) -> Any:
         """Copy ``inputs`` (leading dim B) and ``slots`` [B] into the bucket's
         static buffers, point the padded rows at ``pad_slots``, replay, and
-        return the outputs cut to B rows (graph.py:150-192)."""
+        return the outputs cut to B rows (graph.py:150-192). With
+        ``validate`` the slots are checked first (``check_slots``)."""
         B = int(slots.shape[0])
         size = bucket_for(self.sizes, B)
         buck = self.buckets[size]
         if B < size and pad_slots is None:
             raise ValueError(f"batch {B} pads bucket {size}; pass pad_slots for the "
                              f"{size - B} scratch rows, or the padding will advance live slots")
+        if validate:
+            self.check_slots(slots, pad_slots, size - B)
         _zip_copy(buck.inputs, inputs, B, pad=B < size)
         buck.slots[:B].copy_(slots)
         if B < size:

@@ -28,6 +28,7 @@ not on the GPU, the call raises.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 from functools import lru_cache
 from pathlib import Path
@@ -50,6 +51,8 @@ _vp, _i32, _i64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
 SIGNATURES = {
     "braid_abi_version": ([], _i32),
     "braid_last_error": ([], ctypes.c_char_p),
+    "braid_set_launch_override": ([_i32, _i32], _i32),
+    "braid_get_launch_override": ([_i32], _i32),
     "braid_gdn_decode": ([_vp, _i32, _i64, _i32, _i32, _i32, _i32, _vp, _i32,
                           _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp], _i32),
     "braid_gdn_decode_raw": ([_vp, _i32, _i64, _i32, _i32, _i32, _i32, _vp, _i32,
@@ -161,6 +164,28 @@ class GDNKernels:
             rc = getattr(self._lib, fn_name)(*args, stream)
         if rc != 0:
             raise RuntimeError(self._lib.braid_last_error().decode())
+
+    # -- launch knobs (measurement / tests) ------------------------------------
+
+    KNOBS = {"decode_xcd_remap": 0, "decode_wgs_per_cu": 1, "prefill_layout": 2,
+             "decode_parts": 3}
+
+    @contextlib.contextmanager
+    def launch_override(self, **knobs):
+        """Force launch-shape choices for the calls inside the block (None:
+        the library's own choice), restoring the previous values after. Only
+        the time changes; every shape gives the same bits."""
+        prev = {}
+        try:
+            for name, val in knobs.items():
+                knob = self.KNOBS[name]
+                prev[knob] = self._lib.braid_get_launch_override(knob)
+                rc = self._lib.braid_set_launch_override(knob, -1 if val is None else int(val))
+                _check(rc == 0, self._lib.braid_last_error().decode())
+            yield
+        finally:
+            for knob, val in prev.items():
+                self._lib.braid_set_launch_override(knob, val)
 
     # -- GDN scans ------------------------------------------------------------
 

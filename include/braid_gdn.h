@@ -50,6 +50,32 @@ int braid_abi_version(void);
 const char* braid_last_error(void);
 
 /*
+ * Launch knobs: overrides of the launch-shape choices the library makes per
+ * launch, for measurement and for tests that force each shape. No entry
+ * point's results depend on them (every shape gives the same bits); only the
+ * time does. No counterpart in the reference, which has one launch shape per
+ * kernel. Each knob starts from its environment variable, read once when the
+ * library loads; -1 (or unset) means "the library's own choice".
+ *
+ *   BRAID_KNOB_DECODE_XCD_REMAP  (BRAID_DECODE_XCD_REMAP)  0 / 1
+ *   BRAID_KNOB_DECODE_WGS_PER_CU (BRAID_DECODE_WGS_PER_CU) 0 uncapped, N
+ *   BRAID_KNOB_PREFILL_LAYOUT    (BRAID_PREFILL_COLS)      1, 2, 4, or 0 planned
+ *   BRAID_KNOB_DECODE_PARTS      (BRAID_DECODE_PARTS)      1, 2 or 4 column parts
+ *
+ * A captured graph keeps the launch shape it was captured with.
+ */
+enum braid_launch_knob {
+  BRAID_KNOB_DECODE_XCD_REMAP = 0,
+  BRAID_KNOB_DECODE_WGS_PER_CU = 1,
+  BRAID_KNOB_PREFILL_LAYOUT = 2,
+  BRAID_KNOB_DECODE_PARTS = 3,
+};
+/* Sets a knob (value < 0 clears it). BRAID_EINVAL for an unknown knob. */
+int braid_set_launch_override(int knob, int value);
+/* The knob's current value, -1 when unset or unknown. */
+int braid_get_launch_override(int knob);
+
+/*
  * Batched GDN decode step, precomputed gates.
  * Replaces gdn_decode (braid/kernels/csrc/gdn_decode.cu:313-360).
  *

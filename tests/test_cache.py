@@ -115,3 +115,29 @@ def test_static_input_copy_pads_with_zeros_and_checks_shapes():
         _zip_copy(dst, {"x": [torch.ones(2, 4)], "y": torch.ones(2, 2)}, 2, pad=True)
     with pytest.raises(ValueError, match="do not match"):
         _zip_copy(dst, {"x": [torch.ones(2, 3)]}, 2, pad=True)
+
+
+def test_replayed_step_validates_its_slots():
+    """A graph replay skips the kernels' eager slot checks, so GraphedDecoder
+    checks what step() copies into the static slot buffer: range, distinct
+    live slots, pad slots in range and apart from the live ones."""
+    from types import SimpleNamespace
+
+    from braid_amd.graph import GraphedDecoder
+
+    gd = GraphedDecoder.__new__(GraphedDecoder)
+    gd.cache = SimpleNamespace(max_slots=10)
+    gd.check_slots(torch.tensor([3, 1, 2]), torch.tensor([9]), 1)
+    gd.check_slots(torch.tensor([3, 1, 2]), torch.tensor([9, 9, 9]), 3)  # scratch may repeat
+    with pytest.raises(ValueError, match=r"slot_idx\[1\] = 10 is out of range \[0, 10\)"):
+        gd.check_slots(torch.tensor([3, 10]), None, 0)
+    with pytest.raises(ValueError, match=r"slot_idx\[0\] = -1 is out of range"):
+        gd.check_slots(torch.tensor([-1]), None, 0)
+    with pytest.raises(ValueError, match="duplicate slot 3.*distinct"):
+        gd.check_slots(torch.tensor([3, 1, 3]), None, 0)
+    with pytest.raises(ValueError, match="pad slot 1 is also a live slot"):
+        gd.check_slots(torch.tensor([3, 1]), torch.tensor([1, 9]), 2)
+    with pytest.raises(ValueError, match=r"pad_slots\[0\] = 12 is out of range"):
+        gd.check_slots(torch.tensor([3, 1]), torch.tensor([12]), 1)
+    with pytest.raises(ValueError, match="pad_slots holds 1 slots; 2 rows"):
+        gd.check_slots(torch.tensor([3, 1]), torch.tensor([9]), 2)

@@ -17,7 +17,8 @@ import pytest
 import torch
 
 import oracle
-from gpu_helpers import ATOL, DEV, RTOL, act_np, gen, to_np_pool, ulp16
+from gpu_helpers import (ATOL, DEV, RTOL, act_np, assert_parity, gen, to_np_pool, torch_gates,
+                         ulp16)
 
 pytestmark = pytest.mark.gpu
 H, G, D, C = 32, 16, 128, 8192
@@ -40,9 +41,17 @@ def step_inputs(B, g, act=torch.bfloat16):
     )
 
 
-def oracle_decode_rows(ref_pool, slots, rows, inp, A, dtb):
-    al, be = oracle.gdn_gates(act_np(inp["a"][rows]), act_np(inp["b"][rows]), A.cpu().numpy(),
-                              dtb.cpu().numpy(), "bf16")
+def oracle_decode_rows(ref_pool, slots, rows, inp, A, dtb, gates="oracle"):
+    """The oracle's decode of `rows`. gates="torch": fed torch's gate
+    spelling (gdn.py:299-300), which the in-kernel gates equal bit for bit,
+    so the result is held to the max-abs bar; "oracle": the oracle's own
+    gate restatement."""
+    if gates == "torch":
+        ta, tb = torch_gates(inp["a"][rows], inp["b"][rows], A, dtb)
+        al, be = ta.cpu().numpy(), tb.cpu().numpy()
+    else:
+        al, be = oracle.gdn_gates(act_np(inp["a"][rows]), act_np(inp["b"][rows]),
+                                  A.cpu().numpy(), dtb.cpu().numpy(), "bf16")
     return oracle.gdn_decode(ref_pool, slots, inp["q"][rows].cpu().numpy(),
                              inp["k"][rows].cpu().numpy(), inp["v"][rows].cpu().numpy(), al, be,
                              "f16")
@@ -61,18 +70,24 @@ def test_config1_batched_decode_b128_fp16_pool_64_steps(kern):
     rows = [0, 1, 37, 64, 100, 127]
     row_slots = slots[rows].long()
     local = np.arange(len(rows))
-    worst_ulp, worst_y = 0, 0.0
+    worst_ulp, worst_y, worst_abs = 0, 0.0, 0.0
     for step in range(steps):
         inp = step_inputs(B, g)
-        # teacher-forced: one oracle step from the kernel's current state
+        # teacher-forced: one oracle step from the kernel's current state, with
+        # torch's gate spelling (bitwise the kernel's)
         ref_pool = to_np_pool(pool[row_slots])
-        y_ref = oracle_decode_rows(ref_pool, local, rows, inp, A, dtb)
+        y_ref = oracle_decode_rows(ref_pool, local, rows, inp, A, dtb, gates="torch")
         kern.gdn_decode_raw(pool, slots, inp["q"], inp["k"], inp["v"], inp["a"], inp["b"], A,
                             dtb, y)
         d = ulp16(to_np_pool(pool[row_slots]), ref_pool)
         worst_ulp = max(worst_ulp, int(d.max()))
-        err = np.abs(y[rows].cpu().numpy() - y_ref) - (ATOL + RTOL * np.abs(y_ref))
+        yr = y[rows].cpu().numpy()
+        err = np.abs(yr - y_ref) - (ATOL + RTOL * np.abs(y_ref))
         worst_y = max(worst_y, float(err.max()))
+        worst_abs = max(worst_abs, float(np.abs(yr.astype(np.float64) - y_ref).max()))
+    print(f"  config 1, 64 steps: y max-abs {worst_abs:.3e} (bar 2e-5), state within "
+          f"{worst_ulp} fp16 ulp", flush=True)
+    assert worst_abs <= 2e-5, f"y max-abs error {worst_abs:.3e} exceeds 2e-5"
     assert worst_ulp <= 1, f"state beyond one fp16 ulp of the oracle: {worst_ulp}"
     assert worst_y <= 0, f"y beyond tolerance by {worst_y:.3e}"
     assert torch.equal(pool[unused], before_unused), "an unused slot changed"
@@ -162,10 +177,11 @@ def test_config3_mixer_decode_24_layers_b64(kern):
         rows = [0, 17, 63]
         ref_pool = to_np_pool(pool)
         inp = dict(q=q, k=k, v=v, a=a, b=b)
-        y_ref = oracle_decode_rows(ref_pool, slots[rows].cpu().numpy(), rows, inp, A, dtb)
+        y_ref = oracle_decode_rows(ref_pool, slots[rows].cpu().numpy(), rows, inp, A, dtb,
+                                   gates="torch")
         y = torch.empty(B, H, D, device=DEV)
         kern.gdn_decode_raw(pool, slots, q, k, v, a, b, A, dtb, y)
-        np.testing.assert_allclose(y[rows].cpu().numpy(), y_ref, rtol=1e-4, atol=1e-5)
+        assert_parity(y[rows].cpu().numpy(), y_ref, f"config 3 layer {layer} y")
         d = ulp16(to_np_pool(pool)[slots[rows].cpu().numpy()],
                   ref_pool[slots[rows].cpu().numpy()])
         assert d.max() <= 1

@@ -14,7 +14,7 @@ import pytest
 import torch
 
 import oracle
-from gpu_helpers import (ATOL, DEV, KIND, RTOL, assert_free_running_close, assert_pool_close,
+from gpu_helpers import (DEV, KIND, assert_free_running_close, assert_parity, assert_pool_close,
                          pool, prefill_inputs, raw_gates, to_np_pool, torch_gates)
 
 pytestmark = pytest.mark.gpu
@@ -79,11 +79,60 @@ def test_chunk_matches_oracle(kern, dt):
     kern.gdn_prefill(p, slots, inp["q"], inp["k"], inp["v"], inp["alpha"], inp["beta"], y)
     # errors stay at one rounding per token: the update is non-expansive
     # (alpha <= 1, I - beta k k^T with |k| = 1 and beta in [0, 1])
-    np.testing.assert_allclose(y.cpu().numpy(), y_ref, rtol=1e-4, atol=1e-5)
+    # fp32 pools: the stated max-abs bar. Narrow pools store the state after
+    # every token, where a rounding tie may fall one ulp apart on the two
+    # sides and is then carried forward: y is held to 1e-3 max-abs and to the
+    # relative bar rtol 1e-4 / atol 1e-5 over the 17 tokens.
     if dt == torch.float32:
-        np.testing.assert_allclose(p.cpu().numpy(), ref_pool, rtol=1e-4, atol=1e-5)
+        assert_parity(y.cpu().numpy(), y_ref, "y (f32 pool, 17 tokens)", rel=False)
+    else:
+        assert_parity(y.cpu().numpy(), y_ref, f"y ({KIND[dt]} pool, 17 tokens)", maxabs=1e-3,
+                      rel=False)
+        np.testing.assert_allclose(y.cpu().numpy(), y_ref, rtol=1e-4, atol=1e-5)
+    if dt == torch.float32:
+        assert_parity(p.cpu().numpy(), ref_pool, "fp32 state (17 tokens)", rel=False)
     else:
         assert_free_running_close(to_np_pool(p), ref_pool, KIND[dt])
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.float16], ids=["f32-pool", "f16-pool"])
+def test_a_long_chunk_matches_oracle_on_sampled_heads(kern, dt):
+    """640 tokens with raw gates and ragged lengths, checked against the oracle
+    on sampled (row, head) tiles. fp32 pool: y and the final state to max-abs
+    2e-5. fp16 pool: the state within the free-running bound, and y to 1e-3:
+    the two sides store the state through fp16 after every token, a rounding
+    tie may fall one ulp apart (the per-step bar), and such a difference is
+    carried forward, not amplified, by the non-expansive update. The oracle
+    runs the sampled heads alone (H = G = 1), fed torch's gate spelling, which
+    the in-kernel gates equal bit for bit."""
+    B, T, H, Gk = 2, 640, 32, 16
+    inp = prefill_inputs(B, T, H=H, G=Gk, seed=61)
+    a, b, A, dtb = raw_gates((B, T, H), H, torch.bfloat16, seed=62)
+    lens = torch.tensor([T, 517], dtype=torch.int32, device=DEV)
+    slots = torch.tensor([2, 0], dtype=torch.int32, device=DEV)
+    p = pool(3, H=H, dtype=dt, seed=63)
+    before = to_np_pool(p)
+    y = torch.empty(B, T, H, 128, device=DEV)
+    kern.gdn_prefill_raw(p, slots, inp["q"], inp["k"], inp["v"], a, b, A, dtb, y, lens)
+    torch.cuda.synchronize()
+    alpha, beta = torch_gates(a, b, A, dtb)
+    after = to_np_pool(p)
+    for row, head in ((0, 0), (0, 21), (1, 31)):
+        n = int(lens[row])
+        grp = head // (H // Gk)
+        sub = before[int(slots[row]), head][None, None].copy()
+        sl = lambda t, idx: t[row:row + 1, :n, idx:idx + 1].cpu().numpy()
+        y_ref = oracle.gdn_prefill(sub, [0], sl(inp["q"], grp), sl(inp["k"], grp),
+                                   sl(inp["v"], head), sl(alpha, head), sl(beta, head), KIND[dt])
+        assert_parity(y[row:row + 1, :n, head:head + 1].cpu().numpy(), y_ref,
+                      f"y row {row} head {head}, {n} tokens ({KIND[dt]} pool)",
+                      maxabs=2e-5 if dt == torch.float32 else 1e-3, rel=False)
+        got = after[int(slots[row]), head]
+        if dt == torch.float32:
+            assert_parity(got, sub[0, 0], f"fp32 state row {row} head {head}", rel=False)
+        else:
+            assert_free_running_close(got, sub[0, 0], KIND[dt])
+    assert bool((y[1, 517:] == 0).all()), "pad outputs are not 0"
 
 
 def test_a_pad_column_does_not_move_the_state(kern):
@@ -242,19 +291,18 @@ def test_identity_steps_are_exact_up_to_the_sign_of_zero(kern, dt):
     assert torch.equal(pr, pd) and _same_up_to_zero_sign(pr, pd, dt)
 
 
-@pytest.mark.parametrize("cols", ["1", "2", "0", "4"],
+@pytest.mark.parametrize("cols", [1, 2, 0, 4],
                          ids=["split-1col", "whole-2col", "planned", "quarter"])
 @pytest.mark.parametrize("dt", POOL_DTYPES, ids=POOL_IDS)
-def test_both_scan_layouts_are_decode_bit_for_bit(kern, monkeypatch, dt, cols):
+def test_both_scan_layouts_are_decode_bit_for_bit(kern, dt, cols):
     """The launch picks one column per lane (a tile split over two workgroups)
     for small launches, two otherwise, or, for larger ragged batches, a plan
     per row; the quarter layout (one column and 16 rows per lane, a tile over
-    four workgroups) serves the smallest launches (BRAID_PREFILL_COLS = 1, 2,
-    0 or 4 forces each; here the planned launch splits the 40-token row and
+    four workgroups) serves the smallest launches (the prefill_layout knob
+    = 1, 2, 0 or 4 forces each; here the planned launch splits the 40-token row and
     runs the others whole). Every layout
     must equal decode applied T times, with raw gates and ragged seq_lens
     including 0, on every pool type, with zeros at the pad outputs."""
-    monkeypatch.setenv("BRAID_PREFILL_COLS", cols)
     B, T, H, G = 3, 40, 32, 16
     inp = prefill_inputs(B, T, H=H, G=G, seed=21)
     a, b, A, dtb = raw_gates((B, T, H), H, torch.bfloat16, seed=22)
@@ -263,7 +311,8 @@ def test_both_scan_layouts_are_decode_bit_for_bit(kern, monkeypatch, dt, cols):
     pc = pool(7, H=H, dtype=dt)
     ps = pc.clone()
     yc = torch.empty(B, T, H, 128, device=DEV)
-    kern.gdn_prefill_raw(pc, slots, inp["q"], inp["k"], inp["v"], a, b, A, dtb, yc, lens)
+    with kern.launch_override(prefill_layout=cols):
+        kern.gdn_prefill_raw(pc, slots, inp["q"], inp["k"], inp["v"], a, b, A, dtb, yc, lens)
     for t in range(T):
         live = (t < lens).nonzero().flatten()
         if live.numel() == 0:

@@ -162,3 +162,11 @@ def test_padded_batch_needs_scratch_slots():
         gd.step(x, torch.tensor([1, 2, 3], device=DEV))
     with pytest.raises(ValueError, match="exceeds the largest bucket"):
         gd.step(_inputs(L, 5, 1, seed=8), torch.arange(5, device=DEV))
+    # a replay skips the kernels' eager checks, so step() makes them
+    scratch = torch.tensor([7], device=DEV)
+    with pytest.raises(ValueError, match="duplicate slot 1"):
+        gd.step(x, torch.tensor([1, 2, 1], device=DEV), pad_slots=scratch)
+    with pytest.raises(ValueError, match="out of range"):
+        gd.step(x, torch.tensor([1, 2, 8], device=DEV), pad_slots=scratch)
+    with pytest.raises(ValueError, match="also a live slot"):
+        gd.step(x, torch.tensor([1, 2, 7], device=DEV), pad_slots=scratch)
