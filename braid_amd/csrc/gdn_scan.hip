@@ -28,51 +28,60 @@ __global__ void __launch_bounds__(tile_threads(kDecodeCols))
 gdn_decode_kernel(typename Storage<Tag>::T* __restrict__ pool, const int* __restrict__ slot_idx,
                   const float* __restrict__ q, const float* __restrict__ k,
                   const float* __restrict__ v, Gates gates, float* __restrict__ y, int H,
-                  int heads_per_group, long q_row, long k_row, long v_row, int xcd_contiguous) {
+                  int heads_per_group, long q_row, long k_row, long v_row, int xcd_per) {
   constexpr int CPL = kDecodeCols;
   using ST = typename Storage<Tag>::T;
-  const int tix = stream_tile(xcd_contiguous);
+  // Every argument in registers at once: one round of argument reads, not
+  // one per first use.
+  pin_args(pool, slot_idx, q, k, v, y, H, heads_per_group, q_row, k_row, v_row, xcd_per);
+  gates.pin_args();
+  const int tix = stream_tile(xcd_per);
   const int b = tix / H;
   const int h = tix - b * H;
   const int g = h / heads_per_group;
   const LaneMap<CPL, std::is_same<Tag, F32>::value> L(threadIdx.x);
-
-  // The slot comes from device memory, so one captured graph serves any slot
-  // assignment (gdn_decode.cu:230-236).
   __shared__ TileLds lds;
-  const int slot = slot_idx[b];
-  ST* tile = pool + ((size_t)slot * H + h) * (kSS * kHD);
+  __shared__ QKLds qk_lds[kWaves];
 
-  // The gates come through the scalar unit (load_uniform), so their arithmetic
-  // runs while the tile is still in flight. The q/k/v loads go ahead of the
-  // tile too for 16-bit pools (loads complete in issue order, so the norms then
-  // wait only for them); an fp32 pool's body has no registers to spare for
-  // that and issues them after the tile.
+  // Reads in issue order: the slot (the slot map lives in device memory, so
+  // one captured graph serves any slot assignment, gdn_decode.cu:230-236);
+  // the gates' inputs (vector loads, see lane_zero), so their arithmetic runs
+  // while the tile is still in flight (vector loads complete in issue order);
+  // for 16-bit pools q/k/v, so the norms wait only for them; then, once the
+  // slot is known, the tile. An fp32 pool's body has no registers to spare
+  // for early q/k/v and issues them after the tile. The scheduling barriers
+  // keep this order: the slot's round trip overlaps the issue of the others.
   constexpr bool kEarly = !std::is_same<Tag, F32>::value;
-  const GateRaw gr = gates.load_uniform(b, h, H);
+  const int slot = load_uniform(slot_idx + b);
+  const typename Gates::DecodeIn gin = gates.load_decode(b, h, H);
   const float* qg = q + (size_t)b * q_row + (size_t)g * kSS;
   const float* kg = k + (size_t)b * k_row + (size_t)g * kSS;
   const float* vh = v + (size_t)b * v_row + (size_t)h * kHD;
-  QKRaw qkr;
+  float2 q2, k2;
   float vv[CPL];
   if (kEarly) {
-    load_qk(L, qg, kg, qkr);
+    load_qk2(L, qg, kg, q2, k2);
     load_cols(L, vh, vv);
   }
+  __builtin_amdgcn_sched_barrier(0);
+  ST* tile = pool + ((size_t)slot * H + h) * (kSS * kHD);
   Row<Tag, CPL> S[kRowsPerLane];
 #pragma unroll
   for (int i = 0; i < kRowsPerLane; ++i) load_row(S[i], L, tile + (size_t)L.row(i) * kHD);
   if (!kEarly) {
     load_cols(L, vh, vv);
-    load_qk(L, qg, kg, qkr);
+    load_qk2(L, qg, kg, q2, k2);
   }
-
-  publish_gates(L, gates, gr, h, lds);
+  __builtin_amdgcn_sched_barrier(0);
+  // Every wave holds the gate inputs here, so their reads stay where they
+  // were issued rather than moving into the wave that evaluates each gate.
+  Gates::keep(gin);
+  publish_gates(L, gates, gates.raw_of(gin), gates.consts_of(gin), lds);
   QK qk;
-  normalize_qk(qkr, qk);
+  normalize_qk_lds(L, q2, k2, qk_lds[L.wave], qk);
 
   float yy[CPL];
-  gdn_token<Tag, CPL>(L, S, qk, vv, lds, lds.gate, yy);
+  gdn_token<Tag, CPL>(L, S, qk, vv, lds, yy);
 
 #pragma unroll
   for (int i = 0; i < kRowsPerLane; ++i) store_row(S[i], L, tile + (size_t)L.row(i) * kHD);
@@ -176,9 +185,10 @@ __device__ __forceinline__ void conv_decode_body(typename Storage<Tag>::T* __res
   load_cols(L, lds.qkv[2 + t], vv);
   QK qk;
   normalize_qk(L, lds.qkv[0], lds.qkv[1], qk);
-  publish_gates(L, gates, gates.load(b, h, 0, H, 1), h, lds.tile[t]);
+  publish_gates(L, gates, gates.load(b, h, 0, H, 1), GateConst{gates.A[h], gates.dt_bias[h]},
+                lds.tile[t]);
   float yy[CPL];
-  gdn_token<Tag, CPL>(L, S, qk, vv, lds.tile[t], lds.tile[t].gate, yy);
+  gdn_token<Tag, CPL>(L, S, qk, vv, lds.tile[t], yy);
 #pragma unroll
   for (int i = 0; i < kRowsPerLane; ++i) store_row(S[i], L, tile + (size_t)L.row(i) * kHD);
   if (L.stores_y()) store_cols(L, y + ((size_t)b * H + h) * kHD, yy);
@@ -744,11 +754,12 @@ int launch_decode(void* pool, int pool_dtype, const int32_t* slot_idx, int B, in
   const dim3 grid((unsigned)B * (unsigned)H), block(tile_threads(kDecodeCols));
   const int hpg = H / G;
   const StreamShape shape =
-      stream_shape((long)B * H, device_cus(), pool_dtype != BRAID_F32, sizeof(TileLds),
+      stream_shape((long)B * H, device_cus(), pool_dtype != BRAID_F32,
+                   sizeof(TileLds) + kWaves * sizeof(QKLds),
                    launch_knob(BRAID_KNOB_DECODE_XCD_REMAP),
                    launch_knob(BRAID_KNOB_DECODE_WGS_PER_CU));
   const size_t lds_pad = shape.lds_pad;
-  const int xr = shape.xcd_contiguous;
+  const int xr = shape.xcd_per;
   switch (pool_dtype) {
     case BRAID_F32:
       gdn_decode_kernel<F32, Gates><<<grid, block, lds_pad, stream>>>(

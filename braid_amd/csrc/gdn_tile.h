@@ -294,26 +294,77 @@ struct RowPair1<BF16> : RowHalfPair {
   __device__ __forceinline__ void set(float lo, float hi) { raw = pack_bf16x2(lo, hi); }
 };
 
+// N consecutive floats from / to 16-byte-aligned memory (global or LDS).
+template <int N>
+__device__ __forceinline__ void loadN(const float* __restrict__ p, float (&out)[N]) {
+  typedef float vec __attribute__((ext_vector_type(N)));
+  const vec a = *reinterpret_cast<const vec*>(p);
+#pragma unroll
+  for (int c = 0; c < N; ++c) out[c] = a[c];
+}
+
+template <int N>
+__device__ __forceinline__ void storeN(float* __restrict__ p, const float (&in)[N]) {
+  typedef float vec __attribute__((ext_vector_type(N)));
+  vec a;
+#pragma unroll
+  for (int c = 0; c < N; ++c) a[c] = in[c];
+  *reinterpret_cast<vec*>(p) = a;
+}
+
 // ---------------------------------------------------------------------------
 // Cross-lane sums. Butterflies over lane-index bits: partners add the same two
 // operands (a + b == b + a), so after every stage all lanes of a group hold
-// bit-identical partial sums.
+// bit-identical partial sums. Every partner exchange runs on the VALU (DPP
+// and gfx950's permlane swaps), not through the LDS crossbar: a ds_bpermute
+// costs an LDS round trip per stage, and the decode's reductions are a chain
+// of such stages on its critical path.
 
-__device__ __forceinline__ float xor_shuffle(float v, int mask) {
-  return __shfl_xor(v, mask, 64);
+template <int kCtrl>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, 0xf, 0xf, true));
 }
 
-// Sum over all 64 lanes.
+// v + (v of lane xor 1), xor 2: DPP quad_perm [1,0,3,2] and [2,3,0,1].
+__device__ __forceinline__ float add_xor1(float v) { return v + dpp<0xB1>(v); }
+__device__ __forceinline__ float add_xor2(float v) { return v + dpp<0x4E>(v); }
+
+// v + (v of lane xor 4): a lane with bit 2 clear reads lane + 4 (DPP
+// row_shl:4), one with bit 2 set reads lane - 4 (row_shr:4); both stay inside
+// the lane's 16-lane row.
+__device__ __forceinline__ float add_xor4(float v) {
+  const float up = dpp<0x104>(v), down = dpp<0x114>(v);
+  return v + ((__lane_id() & 4) ? down : up);
+}
+
+// v + (v of lane xor 8): DPP row_ror:8 (within each 16-lane row, rotating by
+// 8 is xor 8).
+__device__ __forceinline__ float add_xor8(float v) { return v + dpp<0x128>(v); }
+
+// v + (v of lane xor 16 / xor 32) through v_permlane16_swap /
+// v_permlane32_swap: after the swap of v with itself the two results hold the
+// even and the odd row's (lane block's) value in every lane, so their sum is
+// the pair's sum.
+__device__ __forceinline__ float add_xor16(float v) {
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+__device__ __forceinline__ float add_xor32(float v) {
+  const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+
+// Sum over all 64 lanes: stages xor 1, 2, 4, 8, 16, 32.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) v += xor_shuffle(v, m);
-  return v;
+  return add_xor32(add_xor16(add_xor8(add_xor4(add_xor2(add_xor1(v))))));
 }
 
 // Sum over a wave's four row groups sharing a column chunk (lane bits 4, 5).
 __device__ __forceinline__ float rowgroup_sum(float v) {
-  v += xor_shuffle(v, 16);
-  v += xor_shuffle(v, 32);
+  v += __shfl_xor(v, 16, 64);
+  v += __shfl_xor(v, 32, 64);
   return v;
 }
 
@@ -322,30 +373,54 @@ __device__ __forceinline__ float rowgroup_sum(float v) {
 //
 // Each policy splits into load() — the global reads for (row b, head h,
 // token t) — and eval_alpha() / eval_beta() — the arithmetic — so a scan can
-// issue the next token's reads early, and so one wave can evaluate each gate
-// for the whole tile (publish_gates).
+// issue the next token's reads early. A decode issues the token's gate reads
+// (load_decode: raw values and head constants) first of all its reads and
+// evaluates each gate once per tile (publish_gates).
 struct GateRaw {
   float x0, x1;  // policy-defined raw values
   bool pad;      // a pad column: alpha = 1, beta = 0
 };
 
-// Loads of one value at a wave-uniform address through the scalar unit
-// (s_load): read through the constant address space, which the kernels never
-// write. A scalar load is counted apart from the vector memory queue, so
-// reading a value this way does not wait behind the state tile's loads. A
-// 16-bit value is taken out of its aligned dword (an aligned 4-byte read
-// cannot cross a page, so it cannot fault past the end of the tensor).
-typedef const __attribute__((address_space(4))) uint32_t* const_u32_ptr;
-__device__ __forceinline__ float load_uniform(const float* p) {
-  return __uint_as_float(*reinterpret_cast<const_u32_ptr>(reinterpret_cast<uintptr_t>(p)));
+// A head's gate constants (A[h], dt_bias[h] for raw gates), read once per
+// tile alongside the token's raw values, so that a decode issues every gate
+// read at its start instead of behind the arithmetic that needs it.
+struct GateConst {
+  float A, dt_bias;
+};
+
+// Marks kernel arguments as used here, in scalar registers: the compiler
+// then reads them all in one round instead of each at its first use (a
+// kernel's argument reads are scalar loads, and it waited for each group
+// before issuing the next).
+template <class T>
+__device__ __forceinline__ void pin_arg(const T& x) {
+  asm volatile("" ::"s"(x));
 }
-__device__ __forceinline__ uint32_t load_uniform(const uint16_t* p) {
-  const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-  const uint32_t w = *reinterpret_cast<const_u32_ptr>(a & ~(uintptr_t)3);
-  return (w >> ((a & 2) * 8)) & 0xffffu;
+template <class... Ts>
+__device__ __forceinline__ void pin_args(const Ts&... xs) {
+  (pin_arg(xs), ...);
 }
+
+// A value at a wave-uniform address, read through the scalar unit (s_load,
+// via the constant address space, which the kernels never write): scalar
+// loads are counted apart from the vector memory queue, so a later wait for
+// this value does not wait for the vector loads issued after it.
 __device__ __forceinline__ int load_uniform(const int* p) {
-  return (int)*reinterpret_cast<const_u32_ptr>(reinterpret_cast<uintptr_t>(p));
+  typedef const __attribute__((address_space(4))) int* const_i32_ptr;
+  return *reinterpret_cast<const_i32_ptr>(reinterpret_cast<uintptr_t>(p));
+}
+
+// A zero the compiler cannot prove wave-uniform. An address offset by it
+// is read with a vector load even when the index is uniform: a decode issues
+// its few per-tile reads (gates, head constants) as vector loads ahead of
+// everything else, so they go out back to back and, completing in issue
+// order, arrive before the tile; as scalar loads the compiler issued them
+// one after another, each waiting for the previous, ahead of the tile's
+// loads.
+__device__ __forceinline__ int lane_zero() {
+  int z;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+  return z;
 }
 
 // Gates the caller computed (gdn_decode.cu:102-110): [B, T, H] fp32.
@@ -356,10 +431,27 @@ struct PrecomputedGates {
     const size_t i = ((size_t)b * T + t) * H + h;
     return GateRaw{alpha[i], beta[i], false};
   }
-  // One decode token's gates (T = 1), at a wave-uniform index.
-  __device__ __forceinline__ GateRaw load_uniform(int b, int h, int H) const {
-    const size_t i = (size_t)b * H + h;
-    return GateRaw{braid::load_uniform(alpha + i), braid::load_uniform(beta + i), false};
+  // One decode token's gate reads (T = 1), as vector loads (lane_zero), kept
+  // in their storage form until the tile's reads have been issued.
+  struct DecodeIn {
+    float a, b;
+  };
+  __device__ __forceinline__ void pin_args() const { braid::pin_args(alpha, beta); }
+  __device__ __forceinline__ DecodeIn load_decode(int b, int h, int H) const {
+    const size_t i = (size_t)b * H + h + lane_zero();
+    return DecodeIn{alpha[i], beta[i]};
+  }
+  __device__ __forceinline__ static void keep(const DecodeIn& d) {
+    asm volatile("" ::"v"(d.a), "v"(d.b));
+  }
+  __device__ __forceinline__ GateRaw raw_of(const DecodeIn& d) const {
+    return GateRaw{d.a, d.b, false};
+  }
+  __device__ __forceinline__ GateConst consts_of(const DecodeIn&) const {
+    return GateConst{0.f, 0.f};
+  }
+  __device__ __forceinline__ float alpha_of(const GateRaw& r, const GateConst&) const {
+    return r.x0;
   }
   __device__ __forceinline__ float eval_alpha(const GateRaw& r, int) const { return r.x0; }
   __device__ __forceinline__ float eval_beta(const GateRaw& r) const { return r.x1; }
@@ -405,17 +497,39 @@ struct RawGates {
     const size_t i = ((size_t)b * T + t) * H + h;
     return GateRaw{ActRead<ActTag>::widen(a_raw[i]), ActRead<ActTag>::widen(b_raw[i]), false};
   }
-  __device__ __forceinline__ GateRaw load_uniform(int b, int h, int H) const {
-    const size_t i = (size_t)b * H + h;
-    const bool pad = seq_lens != nullptr && braid::load_uniform(seq_lens + b) <= 0;
-    return GateRaw{ActRead<ActTag>::widen(braid::load_uniform(a_raw + i)),
-                   ActRead<ActTag>::widen(braid::load_uniform(b_raw + i)), pad};
+  // One decode token's gate reads: the raw values and the head's constants,
+  // as vector loads (lane_zero), kept in their storage form until the tile's
+  // reads have been issued (a conversion here would wait for them first).
+  // Decode launches carry no seq_lens (every row is live), so there is no pad
+  // test: a conditional read would put a branch, and a wait, ahead of the
+  // tile's loads.
+  struct DecodeIn {
+    AT a, b;
+    float A, dt_bias;
+  };
+  __device__ __forceinline__ void pin_args() const { braid::pin_args(a_raw, b_raw, A, dt_bias); }
+  __device__ __forceinline__ DecodeIn load_decode(int b, int h, int H) const {
+    const int z = lane_zero();
+    const size_t i = (size_t)b * H + h + z;
+    return DecodeIn{a_raw[i], b_raw[i], A[h + z], dt_bias[h + z]};
+  }
+  __device__ __forceinline__ static void keep(const DecodeIn& d) {
+    asm volatile("" ::"v"(d.a), "v"(d.b), "v"(d.A), "v"(d.dt_bias));
+  }
+  __device__ __forceinline__ GateRaw raw_of(const DecodeIn& d) const {
+    return GateRaw{ActRead<ActTag>::widen(d.a), ActRead<ActTag>::widen(d.b), false};
+  }
+  __device__ __forceinline__ GateConst consts_of(const DecodeIn& d) const {
+    return GateConst{d.A, d.dt_bias};
+  }
+  __device__ __forceinline__ float alpha_of(const GateRaw& r, const GateConst& c) const {
+    if (r.pad) return 1.f;
+    const float x = r.x0 + c.dt_bias;
+    const float sp = x > 20.f ? x : log1pf(expf(x));
+    return expf(c.A * sp);
   }
   __device__ __forceinline__ float eval_alpha(const GateRaw& r, int h) const {
-    if (r.pad) return 1.f;
-    const float x = r.x0 + dt_bias[h];
-    const float sp = x > 20.f ? x : log1pf(expf(x));
-    return expf(A[h] * sp);
+    return alpha_of(r, GateConst{A[h], dt_bias[h]});
   }
   // Live columns of row b: seq_lens[b] clamped to [0, T] (a length beyond T
   // or below 0 is legal, test_gdn_raw_gates.py:234-256), or all T.
@@ -595,27 +709,6 @@ struct ScanLayoutOf<4> {
   using type = ScanMapQuarter;
 };
 
-// Sum with the partner lane xor 8 (within each 16-lane row): DPP row_ror:8.
-__device__ __forceinline__ float add_xor8(float v) {
-  const int p = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xf, 0xf, false);
-  return v + __int_as_float(p);
-}
-
-// Partner exchanges of the scan layout's tree, all VALU (no LDS): lane
-// xor 16 and xor 32 through gfx950's v_permlane16_swap / v_permlane32_swap.
-// After the swap of v with itself, the two results hold the even and the odd
-// row's (lane block's) value in every lane, so their sum is the pair's sum.
-__device__ __forceinline__ float add_xor16(float v) {
-  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
-                                                  false);
-  return __uint_as_float(p[0]) + __uint_as_float(p[1]);
-}
-__device__ __forceinline__ float add_xor32(float v) {
-  const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
-                                                  false);
-  return __uint_as_float(p[0]) + __uint_as_float(p[1]);
-}
-
 // Column total of the scan layout from a lane's four row-group chains:
 // (rg0 + rg1) + (rg2 + rg3) in-lane, then (w0 + w1) + (w2 + w3) across lanes.
 __device__ __forceinline__ float scan_column_sum(float c0, float c1, float c2, float c3) {
@@ -659,6 +752,26 @@ __device__ __forceinline__ void load_qk(const LM& L, const float* __restrict__ q
   }
 }
 
+// q / k elements 2 lane and 2 lane + 1 (what the norms reduce).
+template <class LM>
+__device__ __forceinline__ void load_qk2(const LM& L, const float* __restrict__ q,
+                                         const float* __restrict__ k, float2& q2, float2& k2) {
+  q2 = *reinterpret_cast<const float2*>(q + 2 * L.lane);
+  k2 = *reinterpret_cast<const float2*>(k + 2 * L.lane);
+}
+
+// One wave's normalised q and k, in LDS in the order a lane reads its rows:
+// element r = 32 w + rg + 4 i at [(4 w + rg) * 8 + i], so a lane's eight rows
+// are eight consecutive floats.
+struct QKLds {
+  float q[kSS];
+  float k[kSS];
+};
+
+__device__ __forceinline__ int qk_lds_pos(int r) {
+  return ((r >> 5) * kRowGroups + (r & 3)) * kRowsPerLane + ((r >> 2) & 7);
+}
+
 // 1 / sqrt(sum x^2 + 1e-6) of a [128] vector held as x[2 lane], x[2 lane + 1]
 // by the 64 lanes of a wave; every lane returns the same bits.
 __device__ __forceinline__ float inv_norm(float2 x2) {
@@ -675,6 +788,25 @@ __device__ __forceinline__ void scale_qk(const QKRaw& r, float q_inv, float k_in
 
 __device__ __forceinline__ void normalize_qk(const QKRaw& r, QK& out) {
   scale_qk(r, inv_norm(r.q2), inv_norm(r.k2), out);
+}
+
+// q_hat / k_hat for this lane's rows from the pairs every lane of the wave
+// loaded (load_qk2): the norms by the wave butterfly, each lane scales its
+// two elements (x * factor, the bits scale_qk gives) and writes them to the
+// wave's own LDS copy, and reads back its eight rows. Only this wave touches
+// `buf`, so no workgroup barrier is needed.
+template <class LM>
+__device__ __forceinline__ void normalize_qk_lds(const LM& L, float2 q2, float2 k2, QKLds& buf,
+                                                 QK& out) {
+  const float qi = inv_norm(q2), ki = inv_norm(k2);
+  const int p0 = qk_lds_pos(2 * L.lane), p1 = qk_lds_pos(2 * L.lane + 1);
+  buf.q[p0] = q2.x * qi;
+  buf.q[p1] = q2.y * qi;
+  buf.k[p0] = k2.x * ki;
+  buf.k[p1] = k2.y * ki;
+  const int base = (L.w * kRowGroups + L.rg) * kRowsPerLane;
+  loadN<kRowsPerLane>(&buf.q[base], out.qh);
+  loadN<kRowsPerLane>(&buf.k[base], out.kh);
 }
 
 template <class LM>
@@ -753,22 +885,22 @@ __device__ __forceinline__ void update_state(Row<Tag, CPL> (&S)[kRowsPerLane], c
 
 // One token of the recurrence on this lane's 8 x CPL block. `v` holds the
 // value entries of the lane's columns; `y` receives their outputs (identical
-// in every lane of a column chunk). alpha and beta are read from LDS at
-// `gate` ([alpha, beta]) after the first barrier, so whoever writes them must
-// do so before it (publish_gates). Contains two workgroup barriers, so all
-// waves of the tile must call it together.
+// in every lane of a column chunk). alpha and beta are read from lds.gate
+// after the first barrier, so whoever writes them must do so before it
+// (publish_gates). Contains two workgroup barriers, so all waves of the tile
+// must call it together.
 template <class Tag, int CPL, bool kSplit>
 __device__ __forceinline__ void gdn_token(const LaneMap<CPL, kSplit>& L,
                                           Row<Tag, CPL> (&S)[kRowsPerLane], const QK& qk,
                                           const float (&v)[CPL], TileLds& lds,
-                                          const float* gate, float (&y)[CPL]) {
+                                          float (&y)[CPL]) {
   float kv[CPL];
   kv_partials<Tag, CPL>(S, qk, kv);
   column_sums_post(L, kv, lds.kv);
   __syncthreads();
   column_sums_take(L, kv, lds.kv);
   float acc[CPL];
-  update_state<Tag, CPL>(S, qk, v, kv, gate[0], gate[1], acc);
+  update_state<Tag, CPL>(S, qk, v, kv, lds.gate[0], lds.gate[1], acc);
   column_sums_post(L, acc, lds.y);
   __syncthreads();
   column_sums_take(L, acc, lds.y);
@@ -912,38 +1044,21 @@ __device__ __forceinline__ void scan_token_quarter(RowPair1<Tag> (&P)[kRowsPerLa
   y = add_xor32(add_xor16(add_xor8(ch[0] + ch[1]))) * kYScale;
 }
 
-// Computes one token's gates ONCE per tile and leaves them in lds.gate for
+// Computes one token's gates once per tile and leaves them in lds.gate for
 // gdn_token: wave 0 evaluates alpha (exp, log1p, exp), wave 1 beta (exp and a
-// divide), each from the raw values all waves loaded. The next workgroup
-// barrier publishes them. The arithmetic is the policy's own (eval_alpha /
-// eval_beta), so which wave runs it does not change a bit.
+// divide), from the inputs every wave loaded. The next workgroup barrier
+// publishes them. The
+// arithmetic is the policy's own, so which wave runs it changes no bit.
 template <class Gates, class LM>
 __device__ __forceinline__ void publish_gates(const LM& L, const Gates& gates, const GateRaw& r,
-                                              int h, TileLds& lds) {
+                                              const GateConst& c, TileLds& lds) {
   if (L.wave == 0) {
-    const float a = gates.eval_alpha(r, h);
+    const float a = gates.alpha_of(r, c);
     if (L.lane == 0) lds.gate[0] = a;
   } else if (L.wave == 1) {
     const float bt = gates.eval_beta(r);
     if (L.lane == 0) lds.gate[1] = bt;
   }
-}
-
-template <int N>
-__device__ __forceinline__ void loadN(const float* __restrict__ p, float (&out)[N]) {
-  typedef float vec __attribute__((ext_vector_type(N)));
-  const vec a = *reinterpret_cast<const vec*>(p);
-#pragma unroll
-  for (int c = 0; c < N; ++c) out[c] = a[c];
-}
-
-template <int N>
-__device__ __forceinline__ void storeN(float* __restrict__ p, const float (&in)[N]) {
-  typedef float vec __attribute__((ext_vector_type(N)));
-  vec a;
-#pragma unroll
-  for (int c = 0; c < N; ++c) a[c] = in[c];
-  *reinterpret_cast<vec*>(p) = a;
 }
 
 }  // namespace braid

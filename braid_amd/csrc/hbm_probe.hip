@@ -90,13 +90,13 @@ int braid_probe_stream(int kind, void* base, int64_t n_tiles, const int32_t* til
   const braid::StreamShape sh = braid::stream_shape(n_tiles, cus, true, 4104, remap_env, cap_env);
   if (kind == 0)
     probe_rmw<<<grid, block, sh.lds_pad, s>>>(static_cast<char*>(base), tile_idx,
-                                              sh.xcd_contiguous);
+                                              sh.xcd_per);
   else if (kind == 1)
     probe_read<<<grid, block, sh.lds_pad, s>>>(static_cast<const char*>(base), tile_idx,
-                                               static_cast<u32x4*>(sink), sh.xcd_contiguous);
+                                               static_cast<u32x4*>(sink), sh.xcd_per);
   else
     probe_write<<<grid, block, sh.lds_pad, s>>>(static_cast<char*>(base), tile_idx,
-                                                sh.xcd_contiguous);
+                                                sh.xcd_per);
   return (int)hipGetLastError();
 }
 

@@ -33,15 +33,17 @@ namespace braid {
 
 constexpr int kXcds = 8;
 
-// The tile a workgroup streams (see above).
-__device__ __forceinline__ int stream_tile(int xcd_contiguous) {
-  if (!xcd_contiguous) return blockIdx.x;
-  const int per = gridDim.x / kXcds;
-  return (blockIdx.x % kXcds) * per + blockIdx.x / kXcds;
+// The tile a workgroup streams (see above): `per` = tiles per XCD (n / 8)
+// for the XCD-contiguous order, 0 for dispatch order. Branch-free, from a
+// kernel argument, so the tile index needs no read beyond the kernel's
+// arguments.
+__device__ __forceinline__ int stream_tile(int per) {
+  const int remapped = (blockIdx.x % kXcds) * per + blockIdx.x / kXcds;
+  return per > 0 ? remapped : (int)blockIdx.x;
 }
 
 struct StreamShape {
-  int xcd_contiguous;  // argument of stream_tile
+  int xcd_per;  // argument of stream_tile
   size_t lds_pad;      // dynamic LDS bytes to request
 };
 
@@ -59,7 +61,7 @@ inline StreamShape stream_shape(long n_tiles, int cus, bool narrow, size_t stati
   const bool large = cus > 0 && n_tiles >= 12L * cus;
   StreamShape s{0, 0};
   const bool remap = remap_env >= 0 ? remap_env > 0 : large;
-  s.xcd_contiguous = (remap && n_tiles % kXcds == 0) ? 1 : 0;
+  s.xcd_per = (remap && n_tiles % kXcds == 0) ? (int)(n_tiles / kXcds) : 0;
   const int cap = cap_env >= 0 ? cap_env : (large && narrow ? 3 : 0);
   if (cap > 0) {
     constexpr long kLdsPerCu = 160 * 1024;
