@@ -21,12 +21,47 @@
 // redundant re-reduction — and converts its share. 128-bit loads throughout:
 // eight bf16/fp16 elements (or two vectors of four fp32) per thread-iteration,
 // eight fp8 codes per 64-bit store.
+#include <mutex>
+
 #include "quant_common.h"
 
 namespace braid {
 namespace {
 
 using namespace quant;
+
+// Device scratch of braid_quantize_act_noalloc: the pass-1 partial maxima
+// (at most kMaxBlocks floats, 4 KiB). One copy per GPU, held for the life of
+// the process. Host code never passes `scratch` itself to a kernel (in host
+// code the name is a stand-in, not a device address): it passes the address
+// hipGetSymbolAddress returned for the current device.
+static __device__ __align__(256) float scratch[kMaxBlocks];
+constexpr int64_t kScratchFloats = kMaxBlocks;
+
+// Per-device address of `scratch`, looked up once per device with that
+// device current (the first no-alloc call made on it).
+constexpr int kMaxDevices = 64;
+float* g_scratch_dev[kMaxDevices];
+std::mutex g_scratch_mu;
+
+int scratch_for_current_device(float** out) {
+  int dev = 0;
+  int st = hip_status(hipGetDevice(&dev), "hipGetDevice");
+  if (st != BRAID_OK) return st;
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(BRAID_EINVAL, "device ordinal " + std::to_string(dev) + " beyond the " +
+                                  std::to_string(kMaxDevices) + " the no-alloc quantizer serves");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_dev[dev] == nullptr) {
+    void* p = nullptr;
+    st = hip_status(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)),
+                    "hipGetSymbolAddress(quantize scratch)");
+    if (st != BRAID_OK) return st;
+    g_scratch_dev[dev] = static_cast<float*>(p);
+  }
+  *out = g_scratch_dev[dev];
+  return BRAID_OK;
+}
 
 template <class Tag>
 int launch(const void* xv, int64_t n, uint8_t* q, float* scale, float* partial,
@@ -47,6 +82,23 @@ int launch(const void* xv, int64_t n, uint8_t* q, float* scale, float* partial,
 using namespace braid;
 
 extern "C" int braid_quantize_act_workspace(int64_t n) { return n <= 0 ? 1 : blocks_for(n); }
+
+extern "C" int braid_quantize_act_noalloc(const void* x, int x_dtype, int64_t n, uint8_t* q,
+                                          float* scale, void* stream_) {
+  if (n <= 0) return fail(BRAID_EINVAL, "x must not be empty");
+  if (x == nullptr || q == nullptr || scale == nullptr)
+    return fail(BRAID_EINVAL, "x/q/scale must be non-null");
+  if (x_dtype != BRAID_F32 && x_dtype != BRAID_F16 && x_dtype != BRAID_BF16)
+    return fail(BRAID_EINVAL, "activation must be fp32, bf16 or fp16");
+  if (blocks_for(n) > kScratchFloats)
+    return fail(BRAID_EINVAL, "quantize_act_noalloc: " + std::to_string(blocks_for(n)) +
+                                  " partials exceed the " + std::to_string(kScratchFloats) +
+                                  "-float device scratch");
+  float* partial = nullptr;
+  const int st = scratch_for_current_device(&partial);
+  if (st != BRAID_OK) return st;
+  return braid_quantize_act(x, x_dtype, n, q, scale, partial, stream_);
+}
 
 extern "C" int braid_quantize_act(const void* x, int x_dtype, int64_t n, uint8_t* q,
                                   float* scale, float* partial, void* stream_) {

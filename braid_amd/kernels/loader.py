@@ -72,6 +72,7 @@ SIGNATURES = {
                               _vp, _vp, _vp], _i32),
     "braid_quantize_act_workspace": ([_i64], _i32),
     "braid_quantize_act": ([_vp, _i32, _i64, _vp, _vp, _vp, _vp], _i32),
+    "braid_quantize_act_noalloc": ([_vp, _i32, _i64, _vp, _vp, _vp], _i32),
     "braid_gated_rmsnorm_workspace": ([_i64], _i32),
     "braid_fp8_gemm_workspace": ([], ctypes.c_size_t),
     "braid_fp8_gemm": ([_vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _vp, ctypes.c_size_t,
@@ -405,6 +406,22 @@ class GDNKernels:
         self._call("braid_quantize_act", x.device, _ptr(x), _QUANT_DTYPES[x.dtype], n,
                    _ptr(q), _ptr(scale), _ptr(partial))
         return [q, scale]
+
+    def quantize_act_into(self, x: torch.Tensor, q: torch.Tensor, scale: torch.Tensor) -> None:
+        """quantize_act into caller-owned outputs, allocating nothing: q
+        (float8_e4m3fn or uint8, x's element count) and scale (one fp32). The
+        partial maxima live in the library's per-GPU device scratch, so calls
+        that overlap on one GPU race (braid_quantize_act_noalloc)."""
+        _check(x.is_cuda and q.is_cuda and scale.is_cuda, "x, q and scale must be cuda")
+        _check(x.is_contiguous() and q.is_contiguous(), "x and q must be contiguous")
+        _check(x.dtype in _QUANT_DTYPES, "activation must be fp32, bf16 or fp16")
+        _check(q.dtype in (torch.float8_e4m3fn, torch.uint8) and q.numel() == x.numel(),
+               "q must hold x's element count as float8_e4m3fn or uint8")
+        _check(scale.dtype == torch.float32 and scale.numel() == 1, "scale must be one fp32")
+        n = x.numel()
+        _check(n > 0, "x must not be empty")
+        self._call("braid_quantize_act_noalloc", x.device, _ptr(x), _QUANT_DTYPES[x.dtype], n,
+                   _ptr(q), _ptr(scale))
 
     # -- gated RMSNorm readout (+ out_proj input quant) -------------------------
 

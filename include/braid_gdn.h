@@ -225,6 +225,24 @@ int braid_quantize_act(const void* x, int x_dtype, int64_t n, uint8_t* q,
                        float* scale, float* partial, void* stream);
 
 /*
+ * braid_quantize_act without a workspace argument: the pass-1 partial maxima
+ * go to a device scratch array inside the library (1024 floats, 4 KiB, one
+ * copy per GPU, held until the process ends), so the call allocates nothing
+ * and needs no caller buffer beyond x, q and scale. No counterpart in the
+ * reference: it is for callers that cannot allocate, such as code under
+ * graph capture or a serving loop that forbids allocation. Codes and scale
+ * equal braid_quantize_act's bit for bit. Every call on one GPU shares that
+ * GPU's scratch, so calls that overlap on one GPU (different streams, or
+ * different threads) race and must be serialised by the caller; a call fully
+ * rewrites the partials it reads, so nothing needs clearing between calls.
+ * The partial count never exceeds the scratch for any n (it is capped at
+ * 1024); a larger count would be rejected with BRAID_EINVAL. Arguments and
+ * errors otherwise as braid_quantize_act.
+ */
+int braid_quantize_act_noalloc(const void* x, int x_dtype, int64_t n, uint8_t* q,
+                               float* scale, void* stream);
+
+/*
  * Number of fp32 partials braid_gated_rmsnorm_quant needs as workspace for
  * `units` (token, head) units.
  */
