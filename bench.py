@@ -6,11 +6,13 @@ per head, fp32 recurrence math, in-kernel gates from bf16 raw projections) on
 a 160-slot fp16 state pool addressed through a random permutation of 128
 distinct slots. Synthetic inputs, seeded.
 
-Timing: K steps are captured in one hipGraph; the graph is replayed 31 times,
-each replay between two synchronisations and timed alone with events on the
-stream the kernels run on, behind a short GPU busy-wait so that the host has
-queued the replay before the start event fires. `value` and `ms_per_step` are
-the median replay (the reference's measure_graphed, noise_floor.py:52-105). The
+Timing: K steps are captured in one hipGraph between two GPU wall-clock
+stamps (a one-thread kernel writing s_memrealtime, libbraid_probe.so); the
+graph is replayed 31 times, each replay between two synchronisations, and
+timed between its stamps, so the graph's own launch latency (~10 us a replay)
+is not charged to the K steps. `value` and `ms_per_step` are the median
+replay (the reference's measure_graphed, noise_floor.py:52-105, which times
+with events around the replay: that figure is reported beside it). The
 default is COLD: step i runs on pool i % P, with P pools totalling > 1 GiB, so
 neither the L2s nor the 256 MB Infinity Cache hold a state slab when it is
 revisited (a single 160 MiB pool would fit and report above-HBM figures). The
@@ -116,18 +118,68 @@ def make_workload(torch, n_pools, seed=0):
 
 def _busy(torch):
     """Keep the GPU busy for ~0.2 ms so that the host has queued the graph
-    replay behind the start event before the GPU reaches it: the timed
-    region then holds the K steps' GPU time, not the host's submission
-    latency of the graph."""
+    replay behind the start event before the GPU reaches it."""
     torch.cuda._sleep(200_000)
 
 
-def replay_times(torch, graph, reps):
+class GpuClock:
+    """GPU wall-clock stamps inside a captured graph (libbraid_probe.so's
+    braid_probe_clock: a one-thread kernel that writes the constant-rate
+    s_memrealtime counter). A stamp before the first timed launch and one
+    after the last bracket exactly the timed launches on the GPU's own clock,
+    so the graph's launch latency (about 10 us per replay on MI355X, which
+    events around graph.replay() include) stays outside the timed region; the
+    second stamp's kernel runs only after the last timed launch completes."""
+
+    def __init__(self, torch):
+        import ctypes
+
+        from braid_amd.build import PROBE_LIB
+
+        lib = ctypes.CDLL(str(PROBE_LIB))
+        self._stamp = lib.braid_probe_clock
+        self._stamp.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        self._stamp.restype = ctypes.c_int
+        rate = lib.braid_probe_clock_hz
+        rate.restype = ctypes.c_double
+        self.hz = rate()
+        if self.hz <= 0:
+            raise RuntimeError("the GPU wall-clock rate is unknown")
+        self.buf = torch.zeros(2, dtype=torch.int64, device="cuda")
+        self.torch = torch
+
+    def stamp(self, i):
+        rc = self._stamp(self.buf[i:].data_ptr(), self.torch.cuda.current_stream().cuda_stream)
+        if rc != 0:
+            raise RuntimeError(f"braid_probe_clock failed ({rc})")
+
+    def seconds(self):
+        t0, t1 = self.buf.tolist()
+        return (t1 - t0) / self.hz
+
+
+def capture_clocked(torch, clock, body):
+    """A graph of: stamp 0, body(), stamp 1."""
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        clock.stamp(0)
+        body()
+        clock.stamp(1)
+    return graph
+
+
+def replay_times(torch, graph, reps, clock=None):
     """Seconds of each of `reps` replays of `graph`, each bracketed by
-    synchronisations and timed with events on the launch stream."""
+    synchronisations: between the graph's two clock stamps when `clock` is
+    given, else with events on the launch stream around the replay."""
     out = []
     for _ in range(reps):
         torch.cuda.synchronize()
+        if clock is not None:
+            graph.replay()
+            torch.cuda.synchronize()
+            out.append(clock.seconds())
+            continue
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         _busy(torch)
         a.record()
@@ -139,12 +191,15 @@ def replay_times(torch, graph, reps):
 
 
 def time_steps(torch, kern, work, steps, warmup, reps=31):
-    """Capture `steps` decode launches (step i on pool i % P) in one graph
-    and replay it `reps` times, each replay timed alone (the reference's
-    measure_graphed, braid/bench/noise_floor.py:52-105). Returns the median
-    seconds per replay and the per-step spread of the replays."""
+    """Capture `steps` decode launches (step i on pool i % P) in one graph,
+    bracketed by GPU clock stamps, and replay it `reps` times, each replay
+    timed alone (the reference's measure_graphed, braid/bench/noise_floor.py
+    :52-105, on the GPU's clock). Returns the median seconds for the `steps`
+    launches and the per-step spread, with the event-timed figure of the same
+    replays (graph launch latency included) beside it."""
     pools, slot_maps, inputs, A, dtb = work
     P = len(pools)
+    clock = GpuClock(torch)
 
     def launch(i):
         p = i % P
@@ -155,20 +210,19 @@ def time_steps(torch, kern, work, steps, warmup, reps=31):
     for i in range(warmup):
         launch(i)
     torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        for i in range(steps):
-            launch(i)
+    graph = capture_clocked(torch, clock, lambda: [launch(i) for i in range(steps)])
     graph.replay()                       # untimed: first replay uploads the graph
     torch.cuda.synchronize()
-    times = replay_times(torch, graph, reps)
+    times = replay_times(torch, graph, reps, clock)
+    ev = sorted(replay_times(torch, graph, 11))
     first = times[0]
     times.sort()
     q = lambda f: round(times[min(len(times) - 1, int(f * len(times)))] * 1e6 / steps, 3)
     median = times[len(times) // 2]
     return median, {"reps": reps, "steps_per_rep": steps, "p10_us": q(0.1),
                     "p50_us": q(0.5), "p90_us": q(0.9),
-                    "first_rep_us": round(first * 1e6 / steps, 3)}
+                    "first_rep_us": round(first * 1e6 / steps, 3),
+                    "event_timed_p50_us": round(ev[len(ev) // 2] * 1e6 / steps, 3)}
 
 
 def copy_bandwidth(torch, nbytes=2 ** 30):
@@ -231,13 +285,11 @@ def stream_ceiling(torch, n_pools, launches=256):
         for i in range(2 * n_pools):
             launch(i)
         torch.cuda.synchronize()
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            for i in range(launches):
-                launch(i)
+        clock = GpuClock(torch)
+        graph = capture_clocked(torch, clock, lambda: [launch(i) for i in range(launches)])
         graph.replay()
         torch.cuda.synchronize()
-        t = sorted(replay_times(torch, graph, 5))
+        t = sorted(replay_times(torch, graph, 5, clock))
         secs = t[len(t) // 2] / launches
         out[f"{label}_us"] = round(secs * 1e6, 2)
         out[f"{label}_gbs"] = round(nbytes / secs / 1e9, 1)
@@ -338,10 +390,8 @@ def graph_time(torch, fn, reps=11, inner=1, before_replay=None):
     with torch.cuda.stream(side):
         fn()
     torch.cuda.current_stream().wait_stream(side)
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        for _ in range(inner):
-            fn()
+    clock = GpuClock(torch)
+    graph = capture_clocked(torch, clock, lambda: [fn() for _ in range(inner)])
     if before_replay is not None:
         before_replay()
     # Replay for at least 20 ms first: the first replays of a kernel after other
@@ -353,7 +403,7 @@ def graph_time(torch, fn, reps=11, inner=1, before_replay=None):
         graph.replay()
         torch.cuda.synchronize()
         n_warm += 1
-    times = sorted(t / inner for t in replay_times(torch, graph, reps))
+    times = sorted(t / inner for t in replay_times(torch, graph, reps, clock))
     return times[len(times) // 2]
 
 

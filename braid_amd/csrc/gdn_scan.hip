@@ -22,24 +22,37 @@
 namespace braid {
 namespace {
 
-// One decode token for the tile (blockIdx.x = b * H + h).
-template <class Tag, class Gates>
+// One decode token for the tile (workgroup index = (b * H + h) * P + part).
+//
+// P column parts: the tile's 128 columns are split over P workgroups of four
+// waves, part p owning columns [128 p / P, 128 (p + 1) / P) with 8 / P columns
+// per lane. Every column sum runs over rows within the column, so a part
+// needs nothing from the others: each lane keeps the same eight rows and its
+// chains, the row-group butterfly and the cross-wave tree are unchanged, and
+// the results are the one-part layout's bits. Small launches use 2 or 4 parts
+// to spread each tile's arithmetic over more CUs (its latency is the
+// per-lane work, which shrinks with the columns). fp32 pools split a lane's
+// columns into two runs 64 apart only with one part.
+template <class Tag, class Gates, int P>
 __global__ void __launch_bounds__(tile_threads(kDecodeCols))
 gdn_decode_kernel(typename Storage<Tag>::T* __restrict__ pool, const int* __restrict__ slot_idx,
                   const float* __restrict__ q, const float* __restrict__ k,
                   const float* __restrict__ v, Gates gates, float* __restrict__ y, int H,
                   int heads_per_group, long q_row, long k_row, long v_row, int xcd_per) {
-  constexpr int CPL = kDecodeCols;
+  constexpr int CPL = kDecodeCols / P;
+  static_assert(P == 1 || P == 2 || P == 4, "1, 2 or 4 column parts");
   using ST = typename Storage<Tag>::T;
   // Every argument in registers at once: one round of argument reads, not
   // one per first use.
   pin_args(pool, slot_idx, q, k, v, y, H, heads_per_group, q_row, k_row, v_row, xcd_per);
   gates.pin_args();
-  const int tix = stream_tile(xcd_per);
+  const int wg = stream_tile(xcd_per);
+  const int tix = P == 1 ? wg : wg / P;
+  const int part = wg - tix * P;
   const int b = tix / H;
   const int h = tix - b * H;
   const int g = h / heads_per_group;
-  const LaneMap<CPL, std::is_same<Tag, F32>::value> L(threadIdx.x);
+  const LaneMap<CPL, std::is_same<Tag, F32>::value && P == 1> L(threadIdx.x, part);
   __shared__ TileLds lds;
   __shared__ QKLds qk_lds[kWaves];
 
@@ -747,31 +760,69 @@ int device_cus() {
   return cus;
 }
 
+// Column parts of a decode launch (gdn_decode_kernel): 2 when a launch has
+// at most as many tiles as the GPU has CUs, else 1. Measured per step on
+// MI355X (fp16 pool, H = 32, cold slots, graph-replayed), parts 1 / 2 / 4:
+// B=1 4.23 / 3.51 / 3.65 us, B=4 4.61 / 3.89 / 5.21, B=8 5.31 / 4.97 / 7.87,
+// B=16 7.15 / 8.28 / 12.54. Four parts never win: two columns per lane make
+// every state access 4 bytes. The DECODE_PARTS launch knob (1, 2 or 4)
+// overrides the choice.
+int decode_parts(long n_tiles, int cus) {
+  const int forced = launch_knob(BRAID_KNOB_DECODE_PARTS);
+  if (forced == 1 || forced == 2 || forced == 4) return forced;
+  return cus > 0 && n_tiles <= cus ? 2 : 1;
+}
+
+template <class Tag, class Gates, int P>
+void launch_decode_as(void* pool, const int32_t* slot_idx, int B, int H, int G, const float* q,
+                      int64_t q_row, const float* k, int64_t k_row, const float* v,
+                      int64_t v_row, Gates gates, float* y, int cus, hipStream_t stream) {
+  const long n_wg = (long)B * H * P;
+  const dim3 grid((unsigned)n_wg), block(tile_threads(kDecodeCols));
+  const StreamShape shape =
+      stream_shape(n_wg, cus, !std::is_same<Tag, F32>::value,
+                   sizeof(TileLds) + kWaves * sizeof(QKLds),
+                   launch_knob(BRAID_KNOB_DECODE_XCD_REMAP),
+                   launch_knob(BRAID_KNOB_DECODE_WGS_PER_CU));
+  gdn_decode_kernel<Tag, Gates, P><<<grid, block, shape.lds_pad, stream>>>(
+      static_cast<typename Storage<Tag>::T*>(pool), slot_idx, q, k, v, gates, y, H, H / G, q_row,
+      k_row, v_row, shape.xcd_per);
+}
+
+template <class Tag, class Gates>
+void launch_decode_parts(int parts, void* pool, const int32_t* slot_idx, int B, int H, int G,
+                         const float* q, int64_t q_row, const float* k, int64_t k_row,
+                         const float* v, int64_t v_row, Gates gates, float* y, int cus,
+                         hipStream_t stream) {
+  if (parts == 4)
+    launch_decode_as<Tag, Gates, 4>(pool, slot_idx, B, H, G, q, q_row, k, k_row, v, v_row,
+                                    gates, y, cus, stream);
+  else if (parts == 2)
+    launch_decode_as<Tag, Gates, 2>(pool, slot_idx, B, H, G, q, q_row, k, k_row, v, v_row,
+                                    gates, y, cus, stream);
+  else
+    launch_decode_as<Tag, Gates, 1>(pool, slot_idx, B, H, G, q, q_row, k, k_row, v, v_row,
+                                    gates, y, cus, stream);
+}
+
 template <class Gates>
 int launch_decode(void* pool, int pool_dtype, const int32_t* slot_idx, int B, int H, int G,
                   const float* q, int64_t q_row, const float* k, int64_t k_row, const float* v,
                   int64_t v_row, Gates gates, float* y, hipStream_t stream) {
-  const dim3 grid((unsigned)B * (unsigned)H), block(tile_threads(kDecodeCols));
-  const int hpg = H / G;
-  const StreamShape shape =
-      stream_shape((long)B * H, device_cus(), pool_dtype != BRAID_F32,
-                   sizeof(TileLds) + kWaves * sizeof(QKLds),
-                   launch_knob(BRAID_KNOB_DECODE_XCD_REMAP),
-                   launch_knob(BRAID_KNOB_DECODE_WGS_PER_CU));
-  const size_t lds_pad = shape.lds_pad;
-  const int xr = shape.xcd_per;
+  const int cus = device_cus();
+  const int parts = decode_parts((long)B * H, cus);
   switch (pool_dtype) {
     case BRAID_F32:
-      gdn_decode_kernel<F32, Gates><<<grid, block, lds_pad, stream>>>(
-          static_cast<float*>(pool), slot_idx, q, k, v, gates, y, H, hpg, q_row, k_row, v_row, xr);
+      launch_decode_parts<F32>(parts, pool, slot_idx, B, H, G, q, q_row, k, k_row, v, v_row,
+                               gates, y, cus, stream);
       break;
     case BRAID_F16:
-      gdn_decode_kernel<F16, Gates><<<grid, block, lds_pad, stream>>>(
-          static_cast<uint16_t*>(pool), slot_idx, q, k, v, gates, y, H, hpg, q_row, k_row, v_row, xr);
+      launch_decode_parts<F16>(parts, pool, slot_idx, B, H, G, q, q_row, k, k_row, v, v_row,
+                               gates, y, cus, stream);
       break;
     default:
-      gdn_decode_kernel<BF16, Gates><<<grid, block, lds_pad, stream>>>(
-          static_cast<uint16_t*>(pool), slot_idx, q, k, v, gates, y, H, hpg, q_row, k_row, v_row, xr);
+      launch_decode_parts<BF16>(parts, pool, slot_idx, B, H, G, q, q_row, k, k_row, v, v_row,
+                                gates, y, cus, stream);
       break;
   }
   const int st = hip_status(hipGetLastError(), "launching gdn_decode_kernel");

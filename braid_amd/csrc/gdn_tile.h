@@ -567,13 +567,15 @@ struct LaneMap {
   int rg;    // row group 0..3
   int cc;    // column chunk within the wave's column group, 0..15
   int col0;  // first of this lane's columns
-  __device__ __forceinline__ LaneMap(int tid) {
+  // part: which kGroupCols-column slice of the tile this workgroup owns, for
+  // a tile split over several workgroups (column parts).
+  __device__ __forceinline__ LaneMap(int tid, int part = 0) {
     lane = tid & 63;
     wave = tid >> 6;
     w = wave % kWaves;
     rg = lane / kLanesPerRowGroup;
     cc = lane % kLanesPerRowGroup;
-    col0 = (wave / kWaves) * kGroupCols + cc * kRun;
+    col0 = (part + wave / kWaves) * kGroupCols + cc * kRun;
   }
   __device__ __forceinline__ int row(int i) const {
     return w * kRowsPerWave + rg + kRowGroups * i;

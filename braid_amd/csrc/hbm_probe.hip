@@ -63,9 +63,36 @@ probe_write(char* base, const int* __restrict__ tile_idx, int xc) {
     __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(t + chunk_offset(i)));
 }
 
+// One thread writes the GPU's constant-rate wall clock (s_memrealtime) to
+// *out. Launched on a stream between other work, it timestamps the point
+// where the work before it has finished (same-stream launches run in order).
+__global__ void __launch_bounds__(64) probe_clock(unsigned long long* out) {
+  if (threadIdx.x == 0) out[0] = __builtin_amdgcn_s_memrealtime();
+}
+
 }  // namespace
 
 extern "C" {
+
+// Enqueues probe_clock on `stream`: *out receives the wall-clock counter when
+// the stream reaches it. Ticks per second: braid_probe_clock_hz(). Returns 0
+// or a nonzero hipError_t.
+int braid_probe_clock(void* out, void* stream) {
+  if (out == nullptr) return (int)hipErrorInvalidValue;
+  probe_clock<<<dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<unsigned long long*>(out));
+  return (int)hipGetLastError();
+}
+
+// Rate of the counter braid_probe_clock reads, in ticks per second (0 if the
+// runtime cannot say).
+double braid_probe_clock_hz(void) {
+  int dev = 0, khz = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess)
+    return 0.0;
+  return 1000.0 * khz;
+}
 
 // One pass over n_tiles 32 KiB tiles at base + tile_idx[t] * 32 KiB, on
 // `stream`. kind 0: read-modify-write in place; 1: read only (sink: 4 KiB of

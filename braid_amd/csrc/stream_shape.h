@@ -13,10 +13,13 @@
 //   51.6 -> 49.4, 75.6 -> 72.6, 100.0 -> 93.8 us; fp32 pool at B = 128:
 //   96.9 -> 95.1 us. Up to B = 64 it changes nothing measurable (B = 8 is 2%
 //   slower), hence the threshold. Needs n % 8 == 0.
-// * Three resident workgroups per CU for 16-bit tiles, not four, by asking for
-//   dynamic LDS the kernel does not use: B = 128 51.7 -> 50.4 us on its own;
-//   with fewer rounds the coarser last round costs more (B = 32: 14.9 ->
-//   16.0 us uncapped vs capped), and fp32 tiles gain nothing.
+// * Two resident workgroups per CU for 16-bit tiles, not four, by asking for
+//   dynamic LDS the kernel does not use. Measured at B = 128 (fp16 pool, cold,
+//   XCD-contiguous), residency cap 2 / 3 / 4 / none: 48.5 / 48.8-49.2 / 49.6 /
+//   49.6 us; the in-place stream probe alone 46.3 / 47.4 / 47.6 / 47.6 us. B =
+//   96: 37.6 / 37.4-37.6 / 38.1 / 38.1 us. Below the threshold the coarser
+//   last round costs more (B = 32: 14.9 -> 16.0 us uncapped vs capped), and
+//   fp32 tiles gain nothing.
 //
 // The caller passes overrides for measurement (-1: no override): remap 0 / 1,
 // cap 0 (uncapped) or N > 0. The kernel library takes them from its launch
@@ -62,7 +65,7 @@ inline StreamShape stream_shape(long n_tiles, int cus, bool narrow, size_t stati
   StreamShape s{0, 0};
   const bool remap = remap_env >= 0 ? remap_env > 0 : large;
   s.xcd_per = (remap && n_tiles % kXcds == 0) ? (int)(n_tiles / kXcds) : 0;
-  const int cap = cap_env >= 0 ? cap_env : (large && narrow ? 3 : 0);
+  const int cap = cap_env >= 0 ? cap_env : (large && narrow ? 2 : 0);
   if (cap > 0) {
     constexpr long kLdsPerCu = 160 * 1024;
     long pad = kLdsPerCu / cap - (long)static_lds - 1024;

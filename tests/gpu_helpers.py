@@ -108,14 +108,28 @@ def assert_parity(got, ref, what: str = "", maxabs: float = MAXABS, rel: bool = 
 
 
 def assert_pool_close(kern_pool: torch.Tensor, ref: np.ndarray, rows, what=""):
-    """fp32 pools within the fp32 tolerance; 16-bit pools within one ulp."""
+    """fp32 pools within the fp32 tolerance; 16-bit pools within one ulp of
+    the element, plus 2^-20 of the slab's rms for elements that cancellation
+    left near zero: the kernel and the oracle sum kv in different fp32
+    orders, which moves a result by ~1e-7 of the state's scale, and that is
+    several ulps of an element a thousand times smaller than the rest (still
+    ~4000x below one ulp at the state's scale)."""
     got = to_np_pool(kern_pool)[rows]
     exp = ref[rows]
     if kern_pool.dtype == torch.float32:
         assert_parity(got, exp, what or "fp32 state")
-    else:
-        d = ulp16(got, exp)
-        assert d.max() <= 1, f"{what}: {int((d > 1).sum())} elements beyond 1 ulp (max {d.max()})"
+        return
+    kind = "f16" if kern_pool.dtype == torch.float16 else "bf16"
+    g = oracle.widen(got, kind).astype(np.float64)
+    r = oracle.widen(exp, kind).astype(np.float64)
+    rms = float(np.sqrt(np.mean(r * r)))
+    bound = ulp_of(r, kind).astype(np.float64) + 2.0 ** -20 * rms
+    err = np.abs(g - r)
+    d = ulp16(got, exp)
+    print(f"  {what or 'narrow state'}: {int((d > 1).sum())} of {d.size} elements beyond 1 ulp "
+          f"(max {int(d.max())}), worst {float((err / bound).max()):.2f}x the bound", flush=True)
+    assert (err <= bound).all(), (f"{what}: {int((err > bound).sum())} elements beyond one ulp "
+                                  f"+ 2^-20 rms")
 
 
 def ulp_of(x: np.ndarray, kind: str) -> np.ndarray:

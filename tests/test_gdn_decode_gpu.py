@@ -343,3 +343,40 @@ def test_launch_shapes_give_identical_bits(kern, dt, H, G):
     y_ref = oracle.gdn_decode(ref_pool, sub, n["q"], n["k"], n["v"],
                               alpha[rows].cpu().numpy(), beta[rows].cpu().numpy(), KIND[dt])
     assert_parity(y0[rows].cpu().numpy(), y_ref, 'y')
+
+
+@pytest.mark.parametrize("dt", POOL_DTYPES, ids=POOL_IDS)
+@pytest.mark.parametrize("B", [1, 3, 8])
+def test_column_parts_give_identical_bits(kern, dt, B):
+    """Small launches split each tile's columns over 2 or 4 workgroups (the
+    decode_parts knob forces 1, 2 or 4). A column's rows, chains and
+    reduction tree do not change, so every split must leave the same pool
+    and y bits as one workgroup per tile; the default launch is also checked
+    against the oracle (torch's gate spelling, max-abs 2e-5)."""
+    H, G = 32, 16
+    slots = torch.randperm(B + 5, generator=torch.Generator().manual_seed(B))[:B]
+    slots = slots.to(torch.int32).to(DEV)
+    inp = decode_inputs(B, H=H, G=G, seed=40 + B)
+    a_raw, b_raw, A, dt_bias = raw_gates((B, H), H, torch.bfloat16, seed=41)
+    base = pool(B + 5, H=H, dtype=dt, seed=42)
+    results = {}
+    for parts in (None, 1, 2, 4):
+        p = base.clone()
+        y = torch.empty(B, H, 128, device=DEV)
+        with kern.launch_override(decode_parts=parts):
+            kern.gdn_decode_raw(p, slots, inp["q"], inp["k"], inp["v"], a_raw, b_raw, A, dt_bias,
+                                y)
+        torch.cuda.synchronize()
+        results[parts] = (p, y)
+    p0, y0 = results[1]
+    for parts, (p, y) in results.items():
+        assert torch.equal(p.view(torch.uint8), p0.view(torch.uint8)), parts
+        assert torch.equal(y, y0), parts
+    pd, yd = results[None]
+    alpha, beta = torch_gates(a_raw, b_raw, A, dt_bias)
+    ref_pool = to_np_pool(base)
+    n = {k: v.cpu().numpy() for k, v in inp.items()}
+    y_ref = oracle.gdn_decode(ref_pool, slots.cpu().numpy(), n["q"], n["k"], n["v"],
+                              alpha.cpu().numpy(), beta.cpu().numpy(), KIND[dt])
+    assert_parity(yd.cpu().numpy(), y_ref, f"y, B={B}, default parts")
+    assert_pool_close(pd, ref_pool, slice(0, B + 5), f"{dt} pool, B={B}")
