@@ -691,6 +691,10 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic},
+        # roofline.traffic: HBM bytes per launch of this kernel from two rocprofv3
+        # counter passes (FETCH_SIZE, WRITE_SIZE) over this command, calibrated on
+        # the stream probes' exact bytes in the same passes
+        "traffic_source": "profiles/gdn_decode_b128_hbm_traffic.md",
         "achieved_gbs": round(achieved, 1),
         "hbm_frac": round(achieved / HBM_PEAK_GBS, 4),
         # value and ms_per_step are the median of these replays (each of all
