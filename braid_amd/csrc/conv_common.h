@@ -70,6 +70,20 @@ __device__ __forceinline__ void store_window(float* st, const float (&w)[K]) {
   }
 }
 
+// The same with the bias value already read (has_bias: a bias is given).
+template <int K>
+__device__ __forceinline__ float conv_step_b(float (&w)[K], float x, const float (&wt)[K],
+                                             float bias, bool has_bias) {
+#pragma unroll
+  for (int i = 0; i < K - 1; ++i) w[i] = w[i + 1];
+  w[K - 1] = x;
+  float acc = w[0] * wt[0];
+#pragma unroll
+  for (int i = 1; i < K; ++i) acc = fmaf(w[i], wt[i], acc);
+  if (has_bias) acc += bias;
+  return silu(acc);
+}
+
 // One token: slide the window, append x, dot with the weight row (in window
 // order, as fmas), add the bias, SiLU.
 template <int K>

@@ -119,6 +119,26 @@ struct ConvDecodeLds {
   float qkv[2 + HPG][kHD];  // conv outputs: q, k, then each head's v
 };
 
+// The decode token of tile t of a conv + decode workgroup, on the conv
+// outputs in LDS (after the barrier that publishes them), then the stores.
+template <class Tag, int HPG, class LM>
+__device__ __forceinline__ void decode_token_from_lds(const LM& L,
+                                                      Row<Tag, kDecodeCols> (&S)[kRowsPerLane],
+                                                      ConvDecodeLds<HPG>& lds, int t,
+                                                      typename Storage<Tag>::T* tile,
+                                                      float* y_row) {
+  constexpr int CPL = kDecodeCols;
+  float vv[CPL];
+  load_cols(L, lds.qkv[2 + t], vv);
+  QK qk;
+  normalize_qk(L, lds.qkv[0], lds.qkv[1], qk);
+  float yy[CPL];
+  gdn_token<Tag, CPL>(L, S, qk, vv, lds.tile[t], yy);
+#pragma unroll
+  for (int i = 0; i < kRowsPerLane; ++i) store_row(S[i], L, tile + (size_t)L.row(i) * kHD);
+  if (L.stores_y()) store_cols(L, y_row, yy);
+}
+
 template <class Tag, class XT, class Gates, int HPG>
 __device__ __forceinline__ void conv_decode_body(typename Storage<Tag>::T* __restrict__ pool,
                                                  float* __restrict__ conv_pool,
@@ -130,26 +150,34 @@ __device__ __forceinline__ void conv_decode_body(typename Storage<Tag>::T* __res
   constexpr int CPL = kDecodeCols, kK = 4;
   constexpr int kTileThreads = tile_threads(CPL);
   using ST = typename Storage<Tag>::T;
+  pin_args(pool, conv_pool, slot_idx, x, conv_w, conv_b, y, H, G, C);
+  gates.pin_args();
   const int b = blockIdx.x / G;
   const int g = blockIdx.x - b * G;
-  const int t = threadIdx.x / kTileThreads;
+  // The conv-first order below serves 16-bit pools with two heads per group
+  // (every Qwen3.5 GDN layer); other shapes load the state first, which their
+  // registers allow without spilling.
+  constexpr bool kConvFirst = sizeof(typename Storage<Tag>::T) == 2 && HPG == 2;
+  // The tile of this wave's threads, uniform in the wave (in the conv-first
+  // order, where the head and the tile's address then live in scalar
+  // registers).
+  const int t = kConvFirst ? __builtin_amdgcn_readfirstlane(threadIdx.x / kTileThreads)
+                           : (int)(threadIdx.x / kTileThreads);
   const int h = g * HPG + t;
   const LaneMap<CPL, std::is_same<Tag, F32>::value> L(threadIdx.x % kTileThreads);
 
   __shared__ ConvDecodeLds<HPG> lds;
-  const int slot = slot_idx[b];
-  ST* tile = pool + ((size_t)slot * H + h) * (kSS * kHD);
 
   // The group's conv channels: segment 0 = q (channels g*SS..), 1 = k
   // (G*SS + g*SS..), 2 + j = v of head g*HPG + j (2*G*SS + head*HD..).
-  // Loads complete in issue order, so for a 16-bit pool the conv's small loads
-  // are issued before the state's and the conv arithmetic then overlaps the
-  // state's arrival; an fp32 tile leaves no registers for that (it would
-  // spill at four waves per SIMD), so there the state is loaded first.
+  // Loads complete in issue order, so in the conv-first order the conv's small
+  // loads are issued before the state's and the conv arithmetic then overlaps
+  // the state's arrival; an fp32 tile, or one head per group (two channels
+  // per thread), leaves no registers for that at four waves per SIMD, so
+  // there the state is loaded first.
   constexpr int kConv = (2 + HPG) * kHD;
   constexpr int kThreads = kTileThreads * HPG;
   constexpr int kPer = (kConv + kThreads - 1) / kThreads;
-  constexpr bool kConvFirst = sizeof(ST) == 2;
   auto channel = [&](int e) {
     const int seg = e / kHD, off = e - seg * kHD;
     return seg < 2 ? seg * G * kSS + g * kSS + off
@@ -157,29 +185,56 @@ __device__ __forceinline__ void conv_decode_body(typename Storage<Tag>::T* __res
   };
   Row<Tag, CPL> S[kRowsPerLane];
   if constexpr (kConvFirst) {
-    float w[kPer][kK], wt[kPer][kK], xv[kPer];
+    // Reads in issue order: the slot (scalar); what does not need it (gate
+    // inputs, conv weights, biases and inputs); then, once the slot is known,
+    // the conv windows and the state. Loads complete in issue order, so the
+    // gate and conv arithmetic overlaps the state's arrival. The scheduling
+    // barriers keep this order.
+    const int slot = load_uniform(slot_idx + b);
+    const typename Gates::DecodeIn gin = gates.load_decode_uniform(b, h, H);
+    float w[kPer][kK], wt[kPer][kK], bv[kPer];
+    XT xr[kPer];  // widened where used: a conversion here would wait for the read
 #pragma unroll
     for (int m = 0; m < kPer; ++m) {
       const int e = threadIdx.x + m * kThreads;
-      if (e < kConv) {
+      if (kConv % kThreads == 0 || e < kConv) {
         const int c = channel(e);
-        load_window<kK>(conv_pool + ((size_t)slot * C + c) * kK, conv_w + (size_t)c * kK, w[m],
-                        wt[m]);
-        xv[m] = conv_widen(x[(size_t)b * C + c]);
+        load_weights<kK>(conv_w + (size_t)c * kK, wt[m]);
+        xr[m] = x[(size_t)b * C + c];
+        bv[m] = conv_b != nullptr ? conv_b[c] : 0.f;
       }
     }
+    __builtin_amdgcn_sched_barrier(0);
+    ST* tile = pool + ((size_t)slot * H + h) * (kSS * kHD);
+    // The slot's windows: a wave-uniform base and a 32-bit per-lane offset,
+    // so the window store needs one vector register for its address.
+    float* const win = conv_pool + (size_t)slot * C * kK;
 #pragma unroll
     for (int i = 0; i < kRowsPerLane; ++i) load_row(S[i], L, tile + (size_t)L.row(i) * kHD);
 #pragma unroll
     for (int m = 0; m < kPer; ++m) {
       const int e = threadIdx.x + m * kThreads;
-      if (e < kConv) {
+      if (kConv % kThreads == 0 || e < kConv)
+        load_weights<kK>(win + (unsigned)channel(e) * kK, w[m]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    Gates::keep_uniform(gin);
+#pragma unroll
+    for (int m = 0; m < kPer; ++m) {
+      const int e = threadIdx.x + m * kThreads;
+      if (kConv % kThreads == 0 || e < kConv) {
         const int c = channel(e), seg = e / kHD;
-        lds.qkv[seg][e - seg * kHD] = conv_step<kK>(w[m], xv[m], wt[m], conv_b, c);
-        store_window<kK>(conv_pool + ((size_t)slot * C + c) * kK, w[m]);
+        lds.qkv[seg][e - seg * kHD] = conv_step_b<kK>(w[m], conv_widen(xr[m]), wt[m], bv[m],
+                                                      conv_b != nullptr);
+        store_window<kK>(win + (unsigned)c * kK, w[m]);
       }
     }
+    publish_gates(L, gates, gates.raw_of(gin), gates.consts_of(gin), lds.tile[t]);
+    __syncthreads();
+    decode_token_from_lds<Tag, HPG>(L, S, lds, t, tile, y + ((size_t)b * H + h) * kHD);
   } else {
+    const int slot = slot_idx[b];
+    ST* tile = pool + ((size_t)slot * H + h) * (kSS * kHD);
 #pragma unroll
     for (int i = 0; i < kRowsPerLane; ++i) load_row(S[i], L, tile + (size_t)L.row(i) * kHD);
     for (int e = threadIdx.x; e < kConv; e += kThreads) {
@@ -191,20 +246,11 @@ __device__ __forceinline__ void conv_decode_body(typename Storage<Tag>::T* __res
                                                   conv_b, c);
       store_window<kK>(st, w);
     }
+    __syncthreads();
+    publish_gates(L, gates, gates.load(b, h, 0, H, 1), GateConst{gates.A[h], gates.dt_bias[h]},
+                  lds.tile[t]);
+    decode_token_from_lds<Tag, HPG>(L, S, lds, t, tile, y + ((size_t)b * H + h) * kHD);
   }
-  __syncthreads();
-
-  float vv[CPL];
-  load_cols(L, lds.qkv[2 + t], vv);
-  QK qk;
-  normalize_qk(L, lds.qkv[0], lds.qkv[1], qk);
-  publish_gates(L, gates, gates.load(b, h, 0, H, 1), GateConst{gates.A[h], gates.dt_bias[h]},
-                lds.tile[t]);
-  float yy[CPL];
-  gdn_token<Tag, CPL>(L, S, qk, vv, lds.tile[t], yy);
-#pragma unroll
-  for (int i = 0; i < kRowsPerLane; ++i) store_row(S[i], L, tile + (size_t)L.row(i) * kHD);
-  if (L.stores_y()) store_cols(L, y + ((size_t)b * H + h) * kHD, yy);
 }
 
 // Two entry kernels over the same body. A 16-bit pool's body fits in 128

@@ -409,6 +409,16 @@ __device__ __forceinline__ int load_uniform(const int* p) {
   typedef const __attribute__((address_space(4))) int* const_i32_ptr;
   return *reinterpret_cast<const_i32_ptr>(reinterpret_cast<uintptr_t>(p));
 }
+__device__ __forceinline__ float load_uniform(const float* p) {
+  return __int_as_float(load_uniform(reinterpret_cast<const int*>(p)));
+}
+// A 16-bit value, taken out of its aligned dword (an aligned 4-byte read
+// cannot cross a page, so it cannot fault past the end of the tensor).
+__device__ __forceinline__ uint16_t load_uniform(const uint16_t* p) {
+  const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+  const uint32_t w = (uint32_t)load_uniform(reinterpret_cast<const int*>(a & ~(uintptr_t)3));
+  return (uint16_t)(w >> ((a & 2) * 8));
+}
 
 // A zero the compiler cannot prove wave-uniform. An address offset by it
 // is read with a vector load even when the index is uniform: a decode issues
@@ -443,6 +453,15 @@ struct PrecomputedGates {
   }
   __device__ __forceinline__ static void keep(const DecodeIn& d) {
     asm volatile("" ::"v"(d.a), "v"(d.b));
+  }
+  // The same reads through the scalar unit, for a wave-uniform h (no vector
+  // registers held); keep_uniform marks them used in scalar registers.
+  __device__ __forceinline__ DecodeIn load_decode_uniform(int b, int h, int H) const {
+    const size_t i = (size_t)b * H + h;
+    return DecodeIn{braid::load_uniform(alpha + i), braid::load_uniform(beta + i)};
+  }
+  __device__ __forceinline__ static void keep_uniform(const DecodeIn& d) {
+    asm volatile("" ::"s"(d.a), "s"(d.b));
   }
   __device__ __forceinline__ GateRaw raw_of(const DecodeIn& d) const {
     return GateRaw{d.a, d.b, false};
@@ -515,6 +534,16 @@ struct RawGates {
   }
   __device__ __forceinline__ static void keep(const DecodeIn& d) {
     asm volatile("" ::"v"(d.a), "v"(d.b), "v"(d.A), "v"(d.dt_bias));
+  }
+  // The same reads through the scalar unit, for a wave-uniform h (no vector
+  // registers held); keep_uniform marks them used in scalar registers.
+  __device__ __forceinline__ DecodeIn load_decode_uniform(int b, int h, int H) const {
+    const size_t i = (size_t)b * H + h;
+    return DecodeIn{braid::load_uniform(a_raw + i), braid::load_uniform(b_raw + i),
+                    braid::load_uniform(A + h), braid::load_uniform(dt_bias + h)};
+  }
+  __device__ __forceinline__ static void keep_uniform(const DecodeIn& d) {
+    asm volatile("" ::"s"(d.a), "s"(d.b), "s"(d.A), "s"(d.dt_bias));
   }
   __device__ __forceinline__ GateRaw raw_of(const DecodeIn& d) const {
     return GateRaw{ActRead<ActTag>::widen(d.a), ActRead<ActTag>::widen(d.b), false};
