@@ -414,7 +414,14 @@ def measure_paths(torch, kern):
     dtb = torch.rand(H, generator=g, device=dev) * 2 - 1
     out = {}
 
+    import ctypes
+    import numpy as np
+
     def prefill_case(lens):
+        """Kernel time of the plan an eager call runs (chosen on the host from
+        seq_lens, braid_prefill_plan), captured with that plan forced; beside
+        it the host's planning time and the time of a captured call, which
+        plans in the kernel."""
         Bp, T = len(lens), max(lens)
         pool = (torch.randn(Bp + 4, H, D, D, generator=g, device=dev) * 0.02).half()
         slots = torch.arange(2, Bp + 2, dtype=torch.int32, device=dev)
@@ -425,13 +432,30 @@ def measure_paths(torch, kern):
         b = torch.randn(Bp, T, H, generator=g, device=dev)
         y = torch.empty(Bp, T, H, D, device=dev)
         sl = torch.tensor(lens, dtype=torch.int32, device=dev)
-        t = graph_time(torch, lambda: kern.gdn_prefill_raw(pool, slots, q, k, v, a, b, A, dtb,
-                                                           y, sl), reps=11)
+        call = lambda: kern.gdn_prefill_raw(pool, slots, q, k, v, a, b, A, dtb, y, sl)
+        host = np.array(lens, dtype=np.int32)
+        cus = torch.cuda.get_device_properties(0).multi_processor_count
+        plan_times = []
+        for _ in range(5):
+            t_plan = time.perf_counter()
+            plan = kern._lib.braid_prefill_plan(host.ctypes.data, Bp, T, H, cus)
+            plan_times.append(time.perf_counter() - t_plan)
+        n4, n2 = plan >> 10, plan & 1023
+        # the launch an eager call makes: one tier for every row runs that
+        # layout's own kernel, otherwise the planned kernel with this plan
+        knobs = ({"prefill_layout": 4} if n4 == Bp else {"prefill_layout": 1} if n2 == Bp
+                 else {"prefill_layout": 0, "prefill_plan": plan})
+        with kern.launch_override(**knobs):
+            t = graph_time(torch, call, reps=11)
+        t_dev = graph_time(torch, call, reps=11)
         tok = sum(lens)
         tf = tok * H * FLOP_PER_TOKEN_HEAD / t / 1e12
         return {"rows": Bp, "max_T": T, "tokens": tok, "ms": round(t * 1e3, 3),
                 "tokens_per_s": round(tok / t, 1), "tflops": round(tf, 2),
-                "fp32_frac": round(tf / FP32_PEAK_TFLOPS, 4)}
+                "fp32_frac": round(tf / FP32_PEAK_TFLOPS, 4),
+                "plan": {"quarter_rows": plan >> 10, "split_rows": plan & 1023},
+                "host_plan_us": round(min(plan_times) * 1e6, 1),
+                "captured_kernel_plan_ms": round(t_dev * 1e3, 3)}
 
     # the config-1 step on bf16 and fp32 pools (one 160-slot pool each; an fp32
     # pool is 320 MiB, past the 256 MB MALL; the bf16 pool's figure is hot)

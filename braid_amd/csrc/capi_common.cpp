@@ -10,9 +10,10 @@ namespace braid {
 namespace {
 thread_local std::string g_last_error;
 
-constexpr int kKnobs = 4;
+constexpr int kKnobs = 5;
 const char* const kKnobEnv[kKnobs] = {"BRAID_DECODE_XCD_REMAP", "BRAID_DECODE_WGS_PER_CU",
-                                      "BRAID_PREFILL_COLS", "BRAID_DECODE_PARTS"};
+                                      "BRAID_PREFILL_COLS", "BRAID_DECODE_PARTS",
+                                      "BRAID_PREFILL_PLAN"};
 
 // Read once, at library load (static initialisation), not per launch.
 struct Knobs {

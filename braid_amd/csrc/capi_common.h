@@ -33,7 +33,8 @@ int validate_slots(const int32_t* slot_idx, int B, int64_t n_slots, bool distinc
 // Launch knobs, for measurement: overrides of the launch-shape choices,
 // -1 when unset. Initialised once from the environment when the library
 // loads (BRAID_DECODE_XCD_REMAP, BRAID_DECODE_WGS_PER_CU, BRAID_PREFILL_COLS,
-// BRAID_DECODE_PARTS), then changed only by braid_set_launch_override.
+// BRAID_DECODE_PARTS, BRAID_PREFILL_PLAN), then changed only by
+// braid_set_launch_override.
 int launch_knob(int knob);
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }

@@ -10,6 +10,10 @@
 // registers (in the pool's storage type) and stores it once. Reference behaviour: braid/kernels/csrc/gdn_decode.cu:156-272 (decode)
 // and :467-551 (prefill); entry-point contracts :313-441 and :553-699.
 #include <algorithm>
+#include <cmath>
+#include <functional>
+#include <queue>
+#include <vector>
 #include <atomic>
 #include <cstdlib>
 #include <type_traits>
@@ -674,7 +678,7 @@ gdn_prefill_planned_kernel(typename Storage<Tag>::T* __restrict__ pool,
                            const float* __restrict__ q, const float* __restrict__ k,
                            const float* __restrict__ v, Gates gates, float* __restrict__ y,
                            int B, int H, int G, int heads_per_group, int T, int cus,
-                           int max_extra) {
+                           int max_extra, int forced_plan) {
   __shared__ StageLds st;
   __shared__ int lens[kMaxPlanRows];
   __shared__ int order[kMaxPlanRows];  // row of each rank
@@ -725,6 +729,12 @@ gdn_prefill_planned_kernel(typename Storage<Tag>::T* __restrict__ pool,
     }
     plan[0] = b4;
     plan[1] = b2;
+    // A plan forced for measurement (n4 * 1024 + n2; the launch sized the
+    // grid for it).
+    if (forced_plan >= 0) {
+      plan[0] = min(forced_plan >> 10, B);
+      plan[1] = min(forced_plan & 1023, B - plan[0]);
+    }
   }
   __syncthreads();
   const int n4 = plan[0], n2 = plan[1];
@@ -922,37 +932,207 @@ void launch_prefill_cols(void* pool, int pool_dtype, const int32_t* slot_idx, in
 template <class Gates>
 void launch_prefill_planned(void* pool, int pool_dtype, const int32_t* slot_idx, int B, int T,
                             int H, int G, const float* q, const float* k, const float* v,
-                            Gates gates, float* y, int cus, hipStream_t stream) {
+                            Gates gates, float* y, int cus, int forced, hipStream_t stream) {
   // At most one extra workgroup per CU for split tiles; the grid has room for
   // whatever the plan uses (the rest return at once).
   const int max_extra = std::min(cus, 3 * B * H);
-  const dim3 grid((unsigned)(B * H + max_extra)), block(256);
+  // forced: a plan chosen on the host (n4 * 1024 + n2), or -1 for the
+  // kernel's own; the grid holds whichever plan runs.
+  int n_wg = B * H + max_extra;
+  if (forced >= 0) {
+    const int n4 = std::min(forced >> 10, B), n2 = std::min(forced & 1023, B - n4);
+    n_wg = std::max(n_wg, (4 * n4 + 2 * n2 + (B - n4 - n2)) * H);
+  }
+  const dim3 grid((unsigned)n_wg), block(256);
   const int hpg = H / G;
   switch (pool_dtype) {
     case BRAID_F32:
       gdn_prefill_planned_kernel<F32, Gates><<<grid, block, 0, stream>>>(
           static_cast<float*>(pool), slot_idx, q, k, v, gates, y, B, H, G, hpg, T, cus,
-          max_extra);
+          max_extra, forced);
       break;
     case BRAID_F16:
       gdn_prefill_planned_kernel<F16, Gates><<<grid, block, 0, stream>>>(
           static_cast<uint16_t*>(pool), slot_idx, q, k, v, gates, y, B, H, G, hpg, T, cus,
-          max_extra);
+          max_extra, forced);
       break;
     default:
       gdn_prefill_planned_kernel<BF16, Gates><<<grid, block, 0, stream>>>(
           static_cast<uint16_t*>(pool), slot_idx, q, k, v, gates, y, B, H, G, hpg, T, cus,
-          max_extra);
+          max_extra, forced);
       break;
   }
+}
+
+// Host plan of a ragged prefill (the planned kernel's tiers), from the live
+// lengths when the call can read them on the host (an eager call, which
+// copies the slot map there anyway). Each candidate (n4 quarter rows, n2
+// split rows, the rest whole; longest rows first, in the kernel's grid order)
+// is scored by simulating the launch on `cus` CUs of two workgroup slots:
+// workgroup i takes the first slot of CU i, workgroup cus + i the second,
+// later ones the slots as they free (in grid order). A workgroup runs its
+// row's tokens at a per-token cost of its tier, solo or sharing its CU, and
+// the cost changes whenever its partner starts or ends. CUs with the same
+// contents form one class, so a simulation is a few dozen events. The costs,
+// relative, were fitted on MI355X to 535 timed plans over 11 ragged batches
+// (fp16 pool, H = 32), per token: quarter 0.344 solo / 0.50 shared, split
+// 0.42 / 0.55, whole 0.60 / 0.85. Against the best measured plan of each
+// batch the chosen ones were 7.8% slower in sum over the 11; the kernel's
+// own estimate had chosen plans up to 35% slower (config 2: 0.538 against
+// 0.474 ms; 4 rows of ~1000 and ~300 tokens: 0.484 against 0.359 ms).
+struct TierCost {
+  float solo, shared;
+};
+constexpr TierCost kPlanCost[3] = {{0.344f, 0.50f}, {0.42f, 0.55f}, {0.60f, 0.85f}};
+
+struct PlanJob {
+  float rem, solo, shared;  // fraction of the job left; its duration solo / shared
+};
+struct PlanClass {
+  long m;  // CUs in the class
+  int n;   // jobs on each (0..2)
+  PlanJob job[2];
+};
+
+// The simulation's state, kept between candidates so its buffers are
+// allocated once per plan.
+struct PlanSim {
+  struct Row {
+    long count;
+    float solo, shared;
+  };
+  std::vector<Row> rows;
+  size_t qi = 0;  // queue front: the next row with workgroups left
+  std::vector<PlanClass> cls, next, groups, g2;
+
+  // Fills one free slot on each CU of `c` from the queue (grid order),
+  // splitting the class where the queue's rows change; appends to `out`.
+  void fill_slot(PlanClass c, std::vector<PlanClass>& out) {
+    long m = c.m;
+    while (m > 0 && qi < rows.size()) {
+      Row& r = rows[qi];
+      const long t = std::min(m, r.count);
+      PlanClass d = c;
+      d.m = t;
+      d.job[d.n++] = PlanJob{1.f, r.solo, r.shared};
+      out.push_back(d);
+      r.count -= t;
+      m -= t;
+      if (r.count == 0) ++qi;
+    }
+    if (m > 0) {
+      c.m = m;
+      out.push_back(c);
+    }
+  }
+
+  float makespan(const std::vector<int>& sorted_lens, int n4, int n2, int H, int cus) {
+    const int B = (int)sorted_lens.size();
+    rows.clear();
+    qi = 0;
+    for (int r = 0; r < B; ++r) {
+      const int tier = r < n4 ? 0 : (r < n4 + n2 ? 1 : 2);
+      const float L = (float)sorted_lens[r];
+      if (sorted_lens[r] > 0)
+        rows.push_back({(long)(tier == 0 ? 4 : tier == 1 ? 2 : 1) * H,
+                        kPlanCost[tier].solo * L, kPlanCost[tier].shared * L});
+    }
+    next.clear();
+    cls.clear();
+    fill_slot(PlanClass{cus, 0, {}}, next);  // first slots
+    for (const PlanClass& c : next)
+      if (c.n > 0) fill_slot(c, cls);         // second slots
+    float t = 0.f;
+    for (int guard = 0; !cls.empty() && guard < 100000; ++guard) {
+      float dt = INFINITY;
+      for (const PlanClass& c : cls)
+        for (int j = 0; j < c.n; ++j)
+          dt = std::min(dt, c.job[j].rem * (c.n == 1 ? c.job[j].solo : c.job[j].shared));
+      t += dt;
+      next.clear();
+      for (PlanClass c : cls) {
+        int kept = 0;
+        for (int j = 0; j < c.n; ++j) {
+          PlanJob jb = c.job[j];
+          jb.rem -= dt / (c.n == 1 ? jb.solo : jb.shared);
+          if (jb.rem > 1e-6f) c.job[kept++] = jb;
+        }
+        const int freed = c.n - kept;
+        c.n = kept;
+        if (freed == 0) {
+          next.push_back(c);
+          continue;
+        }
+        groups.clear();
+        groups.push_back(c);
+        for (int f = 0; f < freed; ++f) {
+          g2.clear();
+          for (const PlanClass& g : groups) fill_slot(g, g2);
+          groups.swap(g2);
+        }
+        for (const PlanClass& g : groups)
+          if (g.n > 0) next.push_back(g);
+      }
+      cls.swap(next);
+    }
+    return t;
+  }
+};
+
+// The plan (n4 * 1024 + n2) with the least simulated makespan, over n4 <= 6
+// quarter rows and n2 <= 8 split rows (ties: the first found, fewer
+// upgraded rows). A candidate is not simulated when a lower bound already
+// reaches the best plan so far: its longest row in each tier alone and
+// solo, or all its work spread over every slot at the shared costs.
+int host_prefill_plan(const std::vector<int32_t>& seq_lens, int T, int H, int cus) {
+  std::vector<int> lens(seq_lens.size());
+  for (size_t r = 0; r < lens.size(); ++r) lens[r] = std::min(std::max((int)seq_lens[r], 0), T);
+  std::sort(lens.begin(), lens.end(), std::greater<int>());
+  const int B = (int)lens.size();
+  std::vector<double> prefix(B + 1, 0.0);
+  for (int r = 0; r < B; ++r) prefix[r + 1] = prefix[r] + lens[r];
+  PlanSim sim;
+  float best = INFINITY;
+  int plan = 0;
+  for (int n4 = 0; n4 <= std::min(B, 6); ++n4)
+    for (int n2 = 0; n2 <= std::min(B - n4, 8); ++n2) {
+      float bound = 0.f;
+      if (n4 > 0) bound = std::max(bound, kPlanCost[0].solo * lens[0]);
+      if (n2 > 0) bound = std::max(bound, kPlanCost[1].solo * lens[n4]);
+      if (n4 + n2 < B) bound = std::max(bound, kPlanCost[2].solo * lens[n4 + n2]);
+      const double work = H * (4.0 * kPlanCost[0].shared * prefix[n4] +
+                               2.0 * kPlanCost[1].shared * (prefix[n4 + n2] - prefix[n4]) +
+                               kPlanCost[2].shared * (prefix[B] - prefix[n4 + n2]));
+      bound = std::max(bound, (float)(work / (2.0 * cus)));
+      if (bound >= best) continue;
+      const float m = sim.makespan(lens, n4, n2, H, cus);
+      if (m < best) {
+        best = m;
+        plan = n4 * 1024 + n2;
+      }
+    }
+  return plan;
 }
 
 template <class Gates>
 int launch_prefill(void* pool, int pool_dtype, const int32_t* slot_idx, int B, int T, int H,
                    int G, const float* q, const float* k, const float* v, Gates gates,
-                   float* y, hipStream_t stream) {
+                   float* y, const std::vector<int32_t>* host_lens, hipStream_t stream) {
   const int cus = device_cus();
-  const int layout = prefill_layout(B * H, B, gates.ragged(), cus);
+  int layout = prefill_layout(B * H, B, gates.ragged(), cus);
+  // With the live lengths on the host, every ragged batch the planned kernel
+  // takes is planned there. A plan that puts every row in one tier runs that
+  // layout's own kernel instead (its split layout runs token pairs, which
+  // the planned kernel's does not: config 4's 4 x 256 tokens 0.155 ms
+  // planned, 0.132 ms in the split kernel).
+  int host_plan = -1;
+  if (host_lens != nullptr && launch_knob(BRAID_KNOB_PREFILL_LAYOUT) < 0 &&
+      launch_knob(BRAID_KNOB_PREFILL_PLAN) < 0 && B <= kMaxPlanRows && cus > 0 &&
+      B * H <= 4 * cus) {
+    host_plan = host_prefill_plan(*host_lens, T, H, cus);
+    const int n4 = host_plan >> 10, n2 = host_plan & 1023;
+    layout = n4 == B ? 4 : (n2 == B ? 1 : 0);
+  }
   if (layout == 4)
     launch_prefill_cols<Gates, 4>(pool, pool_dtype, slot_idx, B, T, H, G, q, k, v, gates, y,
                                   stream);
@@ -962,9 +1142,14 @@ int launch_prefill(void* pool, int pool_dtype, const int32_t* slot_idx, int B, i
   else if (layout == 2)
     launch_prefill_cols<Gates, 2>(pool, pool_dtype, slot_idx, B, T, H, G, q, k, v, gates, y,
                                   stream);
-  else
+  else {
+    // The PREFILL_PLAN knob (measurement) forces a plan; otherwise an eager
+    // call runs the host's plan and a captured one leaves it to the kernel.
+    int forced = launch_knob(BRAID_KNOB_PREFILL_PLAN);
+    if (forced < 0) forced = host_plan;
     launch_prefill_planned<Gates>(pool, pool_dtype, slot_idx, B, T, H, G, q, k, v, gates, y,
-                                  cus > 0 ? cus : 256, stream);
+                                  cus > 0 ? cus : 256, forced, stream);
+  }
   const int st = hip_status(hipGetLastError(), "launching gdn_prefill_kernel");
   return st != BRAID_OK ? st : ok();
 }
@@ -1052,7 +1237,7 @@ extern "C" int braid_gdn_prefill(void* pool, int pool_dtype, int64_t n_slots, in
   }
   BRAID_TRY(validate_slots(slot_idx, B, n_slots, true, stream));
   return launch_prefill(pool, pool_dtype, slot_idx, B, T, H, G, q, k, v,
-                        PrecomputedGates{alpha, beta}, y, stream);
+                        PrecomputedGates{alpha, beta}, y, nullptr, stream);
 }
 
 extern "C" int braid_gdn_prefill_raw(void* pool, int pool_dtype, int64_t n_slots, int H, int G,
@@ -1072,15 +1257,31 @@ extern "C" int braid_gdn_prefill_raw(void* pool, int pool_dtype, int64_t n_slots
     BRAID_TRY(check_dense(v, "v"));
     BRAID_TRY(check_dense(y, "y"));
   }
+  // An eager call reads the live lengths on the host for the ragged plan: the
+  // copy is ordered before the slot map's and completes with its
+  // synchronisation.
+  std::vector<int32_t> host_lens;
+  int cap_st = BRAID_OK;
+  const bool capturing = stream_capturing(stream, &cap_st);
+  if (cap_st != BRAID_OK) return cap_st;
+  if (seq_lens != nullptr && !capturing && T > 0) {
+    host_lens.resize(B);
+    BRAID_TRY(hip_status(hipMemcpyAsync(host_lens.data(), seq_lens, sizeof(int32_t) * (size_t)B,
+                                        hipMemcpyDeviceToHost, stream),
+                         "copying seq_lens to the host"));
+  }
   BRAID_TRY(validate_slots(slot_idx, B, n_slots, true, stream));
+  const std::vector<int32_t>* lens_p = host_lens.empty() ? nullptr : &host_lens;
   if (act_dtype == BRAID_F32) {
     RawGates<F32> gates{static_cast<const float*>(a_raw), static_cast<const float*>(b_raw), A,
                         dt_bias, seq_lens};
-    return launch_prefill(pool, pool_dtype, slot_idx, B, T, H, G, q, k, v, gates, y, stream);
+    return launch_prefill(pool, pool_dtype, slot_idx, B, T, H, G, q, k, v, gates, y, lens_p,
+                          stream);
   }
   RawGates<BF16> gates{static_cast<const uint16_t*>(a_raw), static_cast<const uint16_t*>(b_raw),
                        A, dt_bias, seq_lens};
-  return launch_prefill(pool, pool_dtype, slot_idx, B, T, H, G, q, k, v, gates, y, stream);
+  return launch_prefill(pool, pool_dtype, slot_idx, B, T, H, G, q, k, v, gates, y, lens_p,
+                        stream);
 }
 
 namespace braid {
@@ -1176,4 +1377,11 @@ extern "C" int braid_gdn_conv_decode_raw(void* pool, int pool_dtype, int64_t n_s
                             A, dt_bias, nullptr});
   return go(RawGates<BF16>{static_cast<const uint16_t*>(a_raw),
                            static_cast<const uint16_t*>(b_raw), A, dt_bias, nullptr});
+}
+
+extern "C" int braid_prefill_plan(const int32_t* seq_lens_host, int B, int T, int H, int cus) {
+  if (seq_lens_host == nullptr || B <= 0 || T < 0 || H <= 0 || cus <= 0)
+    return -fail(BRAID_EINVAL,
+                 "braid_prefill_plan needs host lengths, B > 0, T >= 0, H > 0, cus > 0");
+  return host_prefill_plan(std::vector<int32_t>(seq_lens_host, seq_lens_host + B), T, H, cus);
 }

@@ -53,6 +53,7 @@ SIGNATURES = {
     "braid_last_error": ([], ctypes.c_char_p),
     "braid_set_launch_override": ([_i32, _i32], _i32),
     "braid_get_launch_override": ([_i32], _i32),
+    "braid_prefill_plan": ([_vp, _i32, _i32, _i32, _i32], _i32),
     "braid_gdn_decode": ([_vp, _i32, _i64, _i32, _i32, _i32, _i32, _vp, _i32,
                           _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp], _i32),
     "braid_gdn_decode_raw": ([_vp, _i32, _i64, _i32, _i32, _i32, _i32, _vp, _i32,
@@ -169,7 +170,7 @@ class GDNKernels:
     # -- launch knobs (measurement / tests) ------------------------------------
 
     KNOBS = {"decode_xcd_remap": 0, "decode_wgs_per_cu": 1, "prefill_layout": 2,
-             "decode_parts": 3}
+             "decode_parts": 3, "prefill_plan": 4}
 
     @contextlib.contextmanager
     def launch_override(self, **knobs):

@@ -176,3 +176,29 @@ def test_stream_probe_library_loads_and_rejects_bad_arguments():
     assert fn(0, dummy, 0, dummy, None, None) != 0     # no tiles
     assert fn(3, dummy, 4, dummy, None, None) != 0     # unknown kind
     assert fn(1, dummy, 4, dummy, None, None) != 0     # read pass without a sink
+
+
+def test_host_prefill_plan_picks_the_measured_plans(lib):
+    """braid_prefill_plan: the tiers an eager ragged prefill runs (n4 quarter
+    rows, n2 split rows; returned as n4 * 1024 + n2), chosen by simulating the
+    launch on 256 CUs of two workgroup slots. The expected plans are the
+    choices that measured within a few percent of the best of every plan
+    timed on MI355X (H = 32); they pin the simulation, the cost table and the
+    tie order."""
+    cases = {
+        (454, 610, 334, 542, 393, 861, 814, 65): (1, 5),   # config 2
+        (1003, 300, 1001, 383): (3, 1),
+        (900, 850, 200, 200, 200, 200, 200, 200): (2, 2),
+        (256,) * 16: (0, 0),
+    }
+    for lens, (n4, n2) in cases.items():
+        arr = (ctypes.c_int32 * len(lens))(*lens)
+        p = lib.braid_prefill_plan(arr, len(lens), max(lens), 32, 256)
+        assert (p >> 10, p & 1023) == (n4, n2), lens
+    # one row: all quarter would be the fastest layout; a batch of empty rows plans nothing
+    one = (ctypes.c_int32 * 1)(700)
+    assert lib.braid_prefill_plan(one, 1, 700, 32, 256) >> 10 == 1
+    zeros = (ctypes.c_int32 * 3)(0, 0, 0)
+    assert lib.braid_prefill_plan(zeros, 3, 10, 32, 256) == 0
+    assert lib.braid_prefill_plan(None, 3, 10, 32, 256) == -1
+    assert "host lengths" in _err(lib)

@@ -355,3 +355,42 @@ def test_a_skewed_ragged_batch_is_decode_bit_for_bit(kern):
     assert bool((yc[1:, 32:] == 0).all()), "pad outputs are not 0"
     torch.cuda.synchronize()
     assert torch.equal(pc.view(torch.int16), ps.view(torch.int16))
+
+
+def test_host_planned_eager_prefill_equals_the_captured_one(kern):
+    """An eager ragged prefill runs the plan the host chooses from seq_lens; a
+    captured one cannot read them and plans in the kernel. The plans differ
+    (here the host runs the longest row in the quarter layout and five rows
+    split), the bits may not: states and outputs are equal, and equal to
+    decode applied token by token on a sampled row."""
+    lens_l = [454, 610, 334, 542, 393, 861, 814, 65]
+    B, T, H, G = len(lens_l), max(lens_l), 32, 16
+    inp = prefill_inputs(B, T, H=H, G=G, seed=71)
+    a, b, A, dtb = raw_gates((B, T, H), H, torch.bfloat16, seed=72)
+    lens = torch.tensor(lens_l, dtype=torch.int32, device=DEV)
+    slots = torch.arange(1, B + 1, dtype=torch.int32, device=DEV)
+    base = pool(B + 2, H=H, dtype=torch.float16)
+    pe, ye = base.clone(), torch.empty(B, T, H, 128, device=DEV)
+    kern.gdn_prefill_raw(pe, slots, inp["q"], inp["k"], inp["v"], a, b, A, dtb, ye, lens)
+    pg, yg = base.clone(), torch.empty(B, T, H, 128, device=DEV)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        kern.gdn_prefill_raw(pg, slots, inp["q"], inp["k"], inp["v"], a, b, A, dtb, yg, lens)
+    torch.cuda.current_stream().wait_stream(s)
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(pe.view(torch.int16), pg.view(torch.int16)), "states differ"
+    assert torch.equal(ye, yg), "outputs differ"
+    # the 65-token row against decode token by token
+    r = 7
+    ps = base.clone()
+    for t in range(lens_l[r]):
+        yt = torch.empty(1, H, 128, device=DEV)
+        kern.gdn_decode_raw(ps, slots[r:r + 1].contiguous(), inp["q"][r:r + 1, t].contiguous(),
+                            inp["k"][r:r + 1, t].contiguous(), inp["v"][r:r + 1, t].contiguous(),
+                            a[r:r + 1, t].contiguous(), b[r:r + 1, t].contiguous(), A, dtb, yt)
+        assert torch.equal(yt[0], ye[r, t]), t
+    torch.cuda.synchronize()
+    assert torch.equal(ps[slots[r]].view(torch.int16), pe[slots[r]].view(torch.int16))
