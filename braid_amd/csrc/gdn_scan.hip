@@ -191,9 +191,10 @@ __device__ __forceinline__ void conv_decode_body(typename Storage<Tag>::T* __res
   if constexpr (kConvFirst) {
     // Reads in issue order: the slot (scalar); what does not need it (gate
     // inputs, conv weights, biases and inputs); then, once the slot is known,
-    // the conv windows and the state. Loads complete in issue order, so the
-    // gate and conv arithmetic overlaps the state's arrival. The scheduling
-    // barriers keep this order.
+    // the conv windows and then the state. Loads complete in issue order, so
+    // the gate and conv arithmetic overlaps the state's arrival (windows
+    // ahead of the state: 24 config-3 layers 730.6 -> 720.6 us). The
+    // scheduling barriers keep this order.
     const int slot = load_uniform(slot_idx + b);
     const typename Gates::DecodeIn gin = gates.load_decode_uniform(b, h, H);
     float w[kPer][kK], wt[kPer][kK], bv[kPer];
@@ -214,13 +215,13 @@ __device__ __forceinline__ void conv_decode_body(typename Storage<Tag>::T* __res
     // so the window store needs one vector register for its address.
     float* const win = conv_pool + (size_t)slot * C * kK;
 #pragma unroll
-    for (int i = 0; i < kRowsPerLane; ++i) load_row(S[i], L, tile + (size_t)L.row(i) * kHD);
-#pragma unroll
     for (int m = 0; m < kPer; ++m) {
       const int e = threadIdx.x + m * kThreads;
       if (kConv % kThreads == 0 || e < kConv)
         load_weights<kK>(win + (unsigned)channel(e) * kK, w[m]);
     }
+#pragma unroll
+    for (int i = 0; i < kRowsPerLane; ++i) load_row(S[i], L, tile + (size_t)L.row(i) * kHD);
     __builtin_amdgcn_sched_barrier(0);
     Gates::keep_uniform(gin);
 #pragma unroll
