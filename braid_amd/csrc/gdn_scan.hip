@@ -298,14 +298,18 @@ struct alignas(16) StageLds {
 
 // One thread's share of a stage's global inputs, loaded a whole stage ahead so
 // that the loads are in flight while the previous stage's serial loop runs:
-// wave w holds tokens w, w + waves, ... (q and k as the float2 pair each lane
-// reduces for the norms), and every thread kV4 of the stage's 16-byte v pieces
-// and (thread j < kStage) token j's raw gate values.
+// every thread kV4 of the stage's 16-byte v pieces, lane j of the last two
+// waves token j's raw gate values, and the q and k vectors of the wave's
+// tokens w, w + waves, ... in rounds of four vectors: in round u, the 16-lane
+// row (lane / 16) = 2 x + c holds vector c (0: q, 1: k) of the wave's token
+// 2u + x, each lane eight consecutive elements (8 (lane % 16) ...), as two
+// 16-byte pieces (see write_stage for why).
 template <int kTileWaves>
 struct StageRegs {
   static constexpr int kTok = kStage / kTileWaves;
+  static constexpr int kRounds = kTok / 2;
   static constexpr int kV4 = kStage * (kHD / 4) / (64 * kTileWaves);
-  float2 q[kTok], k[kTok];
+  float4 qk[kRounds][2];
   float4 v[kV4];
   GateRaw gate;
 };
@@ -317,7 +321,9 @@ __device__ __forceinline__ void load_stage(StageRegs<kTileWaves>& r, int wave, i
                                            const float* __restrict__ v, int b, int h, int g,
                                            int H, int G, int T, int t0, int n) {
   constexpr int kThreads = 64 * kTileWaves;
-  if ((int)threadIdx.x < n) r.gate = gates.load(b, h, t0 + threadIdx.x, H, T);
+  // Lane j of each of the last two waves: token j's raw gates (alpha is
+  // evaluated by the first of them, beta by the second).
+  if (wave >= kTileWaves - 2 && lane < n) r.gate = gates.load(b, h, t0 + lane, H, T);
 #pragma unroll
   for (int m = 0; m < StageRegs<kTileWaves>::kV4; ++m) {
     const int e = threadIdx.x + m * kThreads, j = e / (kHD / 4), c4 = e % (kHD / 4);
@@ -325,53 +331,74 @@ __device__ __forceinline__ void load_stage(StageRegs<kTileWaves>& r, int wave, i
       r.v[m] = *reinterpret_cast<const float4*>(v + (((size_t)b * T + t0 + j) * H + h) * kHD +
                                                 4 * c4);
   }
+  const float* const src = ((lane >> 4) & 1) ? k : q;
+  const int x = lane >> 5, e0 = 8 * (lane & 15);
 #pragma unroll
-  for (int m = 0; m < StageRegs<kTileWaves>::kTok; ++m) {
-    const int j = wave + m * kTileWaves;
+  for (int u = 0; u < StageRegs<kTileWaves>::kRounds; ++u) {
+    const int j = wave + (2 * u + x) * kTileWaves;
     if (j < n) {
-      const size_t o = (((size_t)b * T + t0 + j) * G + g) * kSS + 2 * lane;
-      r.q[m] = *reinterpret_cast<const float2*>(q + o);
-      r.k[m] = *reinterpret_cast<const float2*>(k + o);
+      const float* p = src + (((size_t)b * T + t0 + j) * G + g) * kSS + e0;
+      r.qk[u][0] = *reinterpret_cast<const float4*>(p);
+      r.qk[u][1] = *reinterpret_cast<const float4*>(p + 4);
     }
   }
 }
 
 // Turns the prefetched inputs of tokens [t0, t0 + n) into the stage in LDS.
-// Gates: the policy's own arithmetic. q and k: the norm factor with the
-// decode's butterfly (inv_norm), two tokens at a time so the butterflies
-// overlap, and q_hat = q * factor as decode's scale_qk does: the same bits.
+// Gates: the policy's own arithmetic, alpha on one wave and beta on another.
+//
+// q and k: q_hat = q * factor with the decode's factor, inv_norm: 1 /
+// sqrt(S + 1e-6), S the sum of the 64 leaves p_l = x[2l]^2 + x[2l+1]^2 over
+// the butterfly lane xor 1, 2, 4, 8, 16, 32, which is the balanced tree that
+// first adds neighbouring leaves, then neighbouring pairs, and so on. Here a
+// lane holds eight consecutive elements, so it forms four neighbouring leaves
+// and their first two tree levels in-lane, ((p0 + p1) + (p2 + p3)); the other
+// four levels pair neighbouring lanes of its 16-lane row, lane xor 1, 2, 4
+// and 8. The same additions in the same order, so the decode's bits, at about
+// a third of the instructions (one 16-lane row per vector: four vectors per
+// wave instruction, and no exchange across rows).
 template <int kTileWaves, class Gates>
 __device__ __forceinline__ void write_stage(const StageRegs<kTileWaves>& r, int wave, int lane,
                                             const Gates& gates, int h, int n, StageLds& st) {
   constexpr int kThreads = 64 * kTileWaves;
-  if ((int)threadIdx.x < n) {
-    st.gate[threadIdx.x][0] = gates.eval_alpha(r.gate, h);
-    st.gate[threadIdx.x][1] = gates.eval_beta(r.gate);
+  // The gates' transcendental chains on two waves, alpha and beta in
+  // parallel, while the other two start on their norms.
+  if (lane < n) {
+    if (wave == kTileWaves - 2) st.gate[lane][0] = gates.eval_alpha(r.gate, h);
+    if (wave == kTileWaves - 1) st.gate[lane][1] = gates.eval_beta(r.gate);
   }
 #pragma unroll
   for (int m = 0; m < StageRegs<kTileWaves>::kV4; ++m) {
     const int e = threadIdx.x + m * kThreads, j = e / (kHD / 4), c4 = e % (kHD / 4);
     if (j < n) *reinterpret_cast<float4*>(&st.v[j][4 * c4]) = r.v[m];
   }
+  constexpr int kRounds = StageRegs<kTileWaves>::kRounds;
+  const int c = (lane >> 4) & 1, x = lane >> 5, e0 = 8 * (lane & 15);
+  float f[kRounds];
 #pragma unroll
-  for (int m = 0; m < StageRegs<kTileWaves>::kTok; m += 2) {
-    const int j = wave + m * kTileWaves, j2 = j + kTileWaves;
-    if (j >= n) break;
-    const float qi1 = inv_norm(r.q[m]), ki1 = inv_norm(r.k[m]);
-    float qi2 = 0.f, ki2 = 0.f;
-    if (j2 < n) {
-      qi2 = inv_norm(r.q[m + 1]);
-      ki2 = inv_norm(r.k[m + 1]);
-    }
-    *reinterpret_cast<float2*>(&st.qk[j][0][2 * lane]) =
-        make_float2(r.q[m].x * qi1, r.q[m].y * qi1);
-    *reinterpret_cast<float2*>(&st.qk[j][1][2 * lane]) =
-        make_float2(r.k[m].x * ki1, r.k[m].y * ki1);
-    if (j2 < n) {
-      *reinterpret_cast<float2*>(&st.qk[j2][0][2 * lane]) =
-          make_float2(r.q[m + 1].x * qi2, r.q[m + 1].y * qi2);
-      *reinterpret_cast<float2*>(&st.qk[j2][1][2 * lane]) =
-          make_float2(r.k[m + 1].x * ki2, r.k[m + 1].y * ki2);
+  for (int u = 0; u < kRounds; ++u) {
+    const float4 a = r.qk[u][0], b = r.qk[u][1];
+    const float p0 = a.x * a.x + a.y * a.y, p1 = a.z * a.z + a.w * a.w;
+    const float p2 = b.x * b.x + b.y * b.y, p3 = b.z * b.z + b.w * b.w;
+    f[u] = (p0 + p1) + (p2 + p3);
+  }
+#pragma unroll
+  for (int u = 0; u < kRounds; ++u) f[u] = add_xor1(f[u]);
+#pragma unroll
+  for (int u = 0; u < kRounds; ++u) f[u] = add_xor2(f[u]);
+#pragma unroll
+  for (int u = 0; u < kRounds; ++u) f[u] = add_xor4(f[u]);
+#pragma unroll
+  for (int u = 0; u < kRounds; ++u) f[u] = add_xor8(f[u]);
+#pragma unroll
+  for (int u = 0; u < kRounds; ++u) {
+    const int j = wave + (2 * u + x) * kTileWaves;
+    if (j < n) {
+      const float fu = rsqrtf(f[u] + kL2Eps);
+      const float4 a = r.qk[u][0], b = r.qk[u][1];
+      float* dst = &st.qk[j][c][e0];
+      *reinterpret_cast<float4*>(dst) = make_float4(a.x * fu, a.y * fu, a.z * fu, a.w * fu);
+      *reinterpret_cast<float4*>(dst + 4) = make_float4(b.x * fu, b.y * fu, b.z * fu, b.w * fu);
     }
   }
 }
