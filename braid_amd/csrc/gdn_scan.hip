@@ -323,7 +323,7 @@ __device__ __forceinline__ void load_stage(StageRegs<kTileWaves>& r, int wave, i
   constexpr int kThreads = 64 * kTileWaves;
   // Lane j of each of the last two waves: token j's raw gates (alpha is
   // evaluated by the first of them, beta by the second).
-  if (wave >= kTileWaves - 2 && lane < n) r.gate = gates.load(b, h, t0 + lane, H, T);
+  if (wave >= kTileWaves - 2 && lane < n) r.gate = gates.load_live(b, h, t0 + lane, H, T);
 #pragma unroll
   for (int m = 0; m < StageRegs<kTileWaves>::kV4; ++m) {
     const int e = threadIdx.x + m * kThreads, j = e / (kHD / 4), c4 = e % (kHD / 4);
@@ -359,12 +359,13 @@ __device__ __forceinline__ void load_stage(StageRegs<kTileWaves>& r, int wave, i
 // wave instruction, and no exchange across rows).
 template <int kTileWaves, class Gates>
 __device__ __forceinline__ void write_stage(const StageRegs<kTileWaves>& r, int wave, int lane,
-                                            const Gates& gates, int h, int n, StageLds& st) {
+                                            const Gates& gates, const GateConst& gc, int n,
+                                            StageLds& st) {
   constexpr int kThreads = 64 * kTileWaves;
   // The gates' transcendental chains on two waves, alpha and beta in
   // parallel, while the other two start on their norms.
   if (lane < n) {
-    if (wave == kTileWaves - 2) st.gate[lane][0] = gates.eval_alpha(r.gate, h);
+    if (wave == kTileWaves - 2) st.gate[lane][0] = gates.alpha_of(r.gate, gc);
     if (wave == kTileWaves - 1) st.gate[lane][1] = gates.eval_beta(r.gate);
   }
 #pragma unroll
@@ -568,6 +569,9 @@ __device__ __forceinline__ void prefill_tile(typename Storage<Tag>::T* __restric
   // row-group half's).
   int r0 = L.w * kRowsPerWave;
   if constexpr (Layout == 4) r0 += 2 * L.rgh;
+  // The head's gate constants, read once (a read per stage would wait on
+  // memory in the middle of the prologue).
+  const GateConst gc = gates.tile_consts(h);
   StageRegs<kW> pre;
   // (Loads nothing when len == 0; a branch around it costs ~30 VGPRs.)
   load_stage<kW>(pre, L.wave, L.lane, gates, q, k, v, b, h, g, H, G, T, 0, min(kStage, len));
@@ -575,7 +579,7 @@ __device__ __forceinline__ void prefill_tile(typename Storage<Tag>::T* __restric
     const int n = min(kStage, len - t0);
     // Every wave has finished reading the previous stage (the barrier at the
     // end of the stage loop), so it may be overwritten.
-    write_stage<kW>(pre, L.wave, L.lane, gates, h, n, st);
+    write_stage<kW>(pre, L.wave, L.lane, gates, gc, n, st);
     __syncthreads();
     // The next stage's loads fly while this stage's tokens run.
     if (t0 + kStage < len)

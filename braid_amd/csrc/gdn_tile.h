@@ -441,6 +441,12 @@ struct PrecomputedGates {
     const size_t i = ((size_t)b * T + t) * H + h;
     return GateRaw{alpha[i], beta[i], false};
   }
+  // A live token's gates (t below the row's length), and the head's
+  // constants, read once per tile by a scan.
+  __device__ __forceinline__ GateRaw load_live(int b, int h, int t, int H, int T) const {
+    return load(b, h, t, H, T);
+  }
+  __device__ __forceinline__ GateConst tile_consts(int) const { return GateConst{0.f, 0.f}; }
   // One decode token's gate reads (T = 1), as vector loads (lane_zero), kept
   // in their storage form until the tile's reads have been issued.
   struct DecodeIn {
@@ -515,6 +521,15 @@ struct RawGates {
     if (seq_lens != nullptr && t >= seq_lens[b]) return GateRaw{0.f, 0.f, true};
     const size_t i = ((size_t)b * T + t) * H + h;
     return GateRaw{ActRead<ActTag>::widen(a_raw[i]), ActRead<ActTag>::widen(b_raw[i]), false};
+  }
+  // A live token's gates (t below the row's length: no pad test, so no read
+  // of seq_lens), and the head's constants, read once per tile by a scan.
+  __device__ __forceinline__ GateRaw load_live(int b, int h, int t, int H, int T) const {
+    const size_t i = ((size_t)b * T + t) * H + h;
+    return GateRaw{ActRead<ActTag>::widen(a_raw[i]), ActRead<ActTag>::widen(b_raw[i]), false};
+  }
+  __device__ __forceinline__ GateConst tile_consts(int h) const {
+    return GateConst{A[h], dt_bias[h]};
   }
   // One decode token's gate reads: the raw values and the head's constants,
   // as vector loads (lane_zero), kept in their storage form until the tile's
