@@ -1006,16 +1006,17 @@ void launch_prefill_planned(void* pool, int pool_dtype, const int32_t* slot_idx,
 // row's tokens at a per-token cost of its tier, solo or sharing its CU, and
 // the cost changes whenever its partner starts or ends. CUs with the same
 // contents form one class, so a simulation is a few dozen events. The costs,
-// relative, were fitted on MI355X to 535 timed plans over 11 ragged batches
-// (fp16 pool, H = 32), per token: quarter 0.344 solo / 0.50 shared, split
-// 0.42 / 0.55, whole 0.60 / 0.85. Against the best measured plan of each
-// batch the chosen ones were 7.8% slower in sum over the 11; the kernel's
-// own estimate had chosen plans up to 35% slower (config 2: 0.538 against
-// 0.474 ms; 4 rows of ~1000 and ~300 tokens: 0.484 against 0.359 ms).
+// relative, were fitted on MI355X to every plan (n4 <= 6, n2 <= 8) timed over
+// 11 ragged batches (fp16 pool, H = 32), per token: quarter 0.344 solo /
+// 0.451 shared, split 0.389 / 0.46, whole 0.606 / 0.978. Against the best
+// measured plan of each batch the chosen ones are 10% slower in sum over the
+// 11 (at most 5.6%, on one 1024-token row among 15 of 128); the kernel's own
+// estimate had chosen plans up to 35% slower (config 2: 0.538 against 0.474
+// ms; 4 rows of ~1000 and ~300 tokens: 0.484 against 0.359 ms).
 struct TierCost {
   float solo, shared;
 };
-constexpr TierCost kPlanCost[3] = {{0.344f, 0.50f}, {0.42f, 0.55f}, {0.60f, 0.85f}};
+constexpr TierCost kPlanCost[3] = {{0.344f, 0.451f}, {0.389f, 0.46f}, {0.606f, 0.978f}};
 
 struct PlanJob {
   float rem, solo, shared;  // fraction of the job left; its duration solo / shared
