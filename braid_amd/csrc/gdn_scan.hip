@@ -357,7 +357,11 @@ __device__ __forceinline__ void load_stage(StageRegs<kTileWaves>& r, int wave, i
 // and 8. The same additions in the same order, so the decode's bits, at about
 // a third of the instructions (one 16-lane row per vector: four vectors per
 // wave instruction, and no exchange across rows).
-template <int kTileWaves, class Gates>
+//
+// kLaneOrder (the eighth layout): q_hat and k_hat go to LDS in the order its
+// lanes read them, row r at qk_lds_pos(r), so a lane's eight rows (one chain)
+// are eight consecutive floats.
+template <int kTileWaves, bool kLaneOrder, class Gates>
 __device__ __forceinline__ void write_stage(const StageRegs<kTileWaves>& r, int wave, int lane,
                                             const Gates& gates, const GateConst& gc, int n,
                                             StageLds& st) {
@@ -397,9 +401,20 @@ __device__ __forceinline__ void write_stage(const StageRegs<kTileWaves>& r, int 
     if (j < n) {
       const float fu = rsqrtf(f[u] + kL2Eps);
       const float4 a = r.qk[u][0], b = r.qk[u][1];
-      float* dst = &st.qk[j][c][e0];
-      *reinterpret_cast<float4*>(dst) = make_float4(a.x * fu, a.y * fu, a.z * fu, a.w * fu);
-      *reinterpret_cast<float4*>(dst + 4) = make_float4(b.x * fu, b.y * fu, b.z * fu, b.w * fu);
+      float* dst = &st.qk[j][c][0];
+      if constexpr (kLaneOrder) {
+        // Rows e0 + k (e0 a multiple of 8): row block e0 / 32, row group k % 4,
+        // chain index (e0 / 4) % 8 + k / 4.
+        const int base = (e0 >> 5) * (kRowGroups * kRowsPerLane) + ((e0 >> 2) & 7);
+        const float xs[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk)
+          dst[base + (kk & 3) * kRowsPerLane + (kk >> 2)] = xs[kk] * fu;
+      } else {
+        *reinterpret_cast<float4*>(dst + e0) = make_float4(a.x * fu, a.y * fu, a.z * fu, a.w * fu);
+        *reinterpret_cast<float4*>(dst + e0 + 4) =
+            make_float4(b.x * fu, b.y * fu, b.z * fu, b.w * fu);
+      }
     }
   }
 }
@@ -464,6 +479,42 @@ __device__ __forceinline__ void read_token_quarter(const StageLds& st, int j, in
     t.qh[1][i] = q2.y;
   }
 }
+
+// The eighth layout's token: its chain's 8 rows of k_hat / q_hat (two 16-byte
+// reads each, the stage being in lane order), its column's v, and the gates.
+struct TokenInE {
+  float kh[kRowsPerLane], qh[kRowsPerLane];
+  float v, alpha, beta;
+};
+
+__device__ __forceinline__ void read_token_eighth(const StageLds& st, int j, int pos, int col0,
+                                                  TokenInE& t) {
+  const float2 ab = *reinterpret_cast<const float2*>(&st.gate[j][0]);
+  t.alpha = ab.x;
+  t.beta = ab.y;
+  t.v = st.v[j][col0];
+  loadN<kRowsPerLane>(&st.qk[j][1][pos], t.kh);
+  loadN<kRowsPerLane>(&st.qk[j][0][pos], t.qh);
+}
+
+// The eighth layout's state: the lane's chain, rows i = 2m and 2m + 1 in
+// p[m].
+template <class Tag>
+struct ScanStateE {
+  RowPair1<Tag> p[kRowsPerLane / 2];
+  template <class ST>
+  __device__ __forceinline__ void load(const ScanMapEighth& L, const ST* tile) {
+#pragma unroll
+    for (int m = 0; m < kRowsPerLane / 2; ++m)
+      p[m].load_nt(tile + (size_t)L.row(2 * m) * kHD, tile + (size_t)L.row(2 * m + 1) * kHD);
+  }
+  template <class ST>
+  __device__ __forceinline__ void store(const ScanMapEighth& L, ST* tile) const {
+#pragma unroll
+    for (int m = 0; m < kRowsPerLane / 2; ++m)
+      p[m].store_nt(tile + (size_t)L.row(2 * m) * kHD, tile + (size_t)L.row(2 * m + 1) * kHD);
+  }
+};
 
 template <class Tag, int CPL, int kLRG>
 struct ScanState;
@@ -561,7 +612,7 @@ __device__ __forceinline__ void prefill_tile(typename Storage<Tag>::T* __restric
   const int slot = slot_idx[b];
   ST* tile = pool + ((size_t)slot * H + h) * (kSS * kHD) + L.col0;
 
-  ScanState<Tag, CPL, kLRG> S;
+  typename std::conditional<Layout == 8, ScanStateE<Tag>, ScanState<Tag, CPL, kLRG>>::type S;
   S.load(L, tile);
 
   constexpr int kW = LM::kWaves;
@@ -569,6 +620,8 @@ __device__ __forceinline__ void prefill_tile(typename Storage<Tag>::T* __restric
   // row-group half's).
   int r0 = L.w * kRowsPerWave;
   if constexpr (Layout == 4) r0 += 2 * L.rgh;
+  // The eighth layout's chain in the lane-ordered stage.
+  if constexpr (Layout == 8) r0 = (L.w * kRowGroups + L.rg) * kRowsPerLane;
   // The head's gate constants, read once (a read per stage would wait on
   // memory in the middle of the prologue).
   const GateConst gc = gates.tile_consts(h);
@@ -579,7 +632,7 @@ __device__ __forceinline__ void prefill_tile(typename Storage<Tag>::T* __restric
     const int n = min(kStage, len - t0);
     // Every wave has finished reading the previous stage (the barrier at the
     // end of the stage loop), so it may be overwritten.
-    write_stage<kW>(pre, L.wave, L.lane, gates, gc, n, st);
+    write_stage<kW, Layout == 8>(pre, L.wave, L.lane, gates, gc, n, st);
     __syncthreads();
     // The next stage's loads fly while this stage's tokens run.
     if (t0 + kStage < len)
@@ -588,7 +641,27 @@ __device__ __forceinline__ void prefill_tile(typename Storage<Tag>::T* __restric
     float* yt = y + (((size_t)b * T + t0) * H + h) * kHD + L.col0;
     const size_t y_tok = (size_t)H * kHD;
     int j = 0;
-    if constexpr (Layout == 4) {
+    if constexpr (Layout == 8) {
+      for (; j + 1 < n; j += 2) {
+        TokenInE in0, in1;
+        read_token_eighth(st, j, r0, L.col0, in0);
+        read_token_eighth(st, j + 1, r0, L.col0, in1);
+        float y0[1], y1[1];
+        scan_token_eighth<Tag, true>(S.p, in0.kh, in0.qh, in0.v, in0.alpha, in0.beta, y0[0]);
+        scan_token_eighth<Tag, true>(S.p, in1.kh, in1.qh, in1.v, in1.alpha, in1.beta, y1[0]);
+        if (L.stores_y()) {
+          storeN<1>(yt + j * y_tok, y0);
+          storeN<1>(yt + (j + 1) * y_tok, y1);
+        }
+      }
+      for (; j < n; ++j) {
+        TokenInE in;
+        read_token_eighth(st, j, r0, L.col0, in);
+        float yy[1];
+        scan_token_eighth<Tag>(S.p, in.kh, in.qh, in.v, in.alpha, in.beta, yy[0]);
+        if (L.stores_y()) storeN<1>(yt + j * y_tok, yy);
+      }
+    } else if constexpr (Layout == 4) {
       if constexpr (kTokenPairs) {
         for (; j + 1 < n; j += 2) {
           TokenInQ in0, in1;
@@ -636,7 +709,7 @@ __device__ __forceinline__ void prefill_tile(typename Storage<Tag>::T* __restric
         }
       }
     }
-    if constexpr (Layout != 4) {
+    if constexpr (Layout != 4 && Layout != 8) {
       for (; j < n; ++j) {
         TokenIn<CPL> in;
         read_token<CPL>(st, j, r0, L.col0, in);
@@ -662,9 +735,10 @@ __device__ __forceinline__ void prefill_tile(typename Storage<Tag>::T* __restric
   }
 }
 
-// One tile (layout 2), a half tile (layout 1, kParts = 2) or a quarter tile
-// (layout 4, kParts = 4) per workgroup: blockIdx.x = (b * H + h) * kParts +
-// part. Layouts 1 and 4 run token pairs.
+// One tile (layout 2), a half tile (layout 1, kParts = 2), a quarter tile
+// (layout 4, kParts = 4) or an eighth (layout 8, kParts = 8) per workgroup:
+// blockIdx.x = (b * H + h) * kParts + part. Layouts 1, 4 and 8 run token
+// pairs.
 template <class Tag, class Gates, int Layout>
 __global__ void __launch_bounds__(64 * ScanLayoutOf<Layout>::type::kWaves)
 gdn_prefill_kernel(typename Storage<Tag>::T* __restrict__ pool,
@@ -918,8 +992,10 @@ int launch_decode(void* pool, int pool_dtype, const int32_t* slot_idx, int B, in
 }
 
 // Prefill layout of a launch:
+//   8: the eighth layout (one column and 8 rows per lane, eight workgroups
+//      per tile), when that leaves no CU with a second workgroup;
 //   4: the quarter layout (one column and 16 rows per lane, four workgroups
-//      per tile), when that still leaves no CU with a second workgroup;
+//      per tile), likewise;
 //   1: one column per lane for every tile (two workgroups per tile), likewise;
 //   2: two columns per lane for every tile;
 //   0: planned per row from seq_lens (gdn_prefill_planned_kernel), for larger
@@ -927,12 +1003,15 @@ int launch_decode(void* pool, int pool_dtype, const int32_t* slot_idx, int B, in
 // Measured (MI355X, 256 CUs): one 512-token row 0.315 ms in layout 1, 0.225 ms
 // in layout 4; rows (300, 700) 0.425 -> 0.301 ms; config 4's 128 tiles, where
 // layout 4 would put two workgroups on every CU, 0.183 in layout 1 against
-// 0.190 ms. The PREFILL_LAYOUT launch knob (1, 2, 4, or 0 for planned when
-// seq_lens is given) overrides the choice.
+// 0.190 ms; one 512-token row in layout 8 0.126 ms against 0.164 in layout
+// 4, 1024 tokens 0.245 against 0.320 (half the VALU per token again, and the
+// column sums inside 16-lane rows). The PREFILL_LAYOUT launch knob (1, 2, 4,
+// 8, or 0 for planned when seq_lens is given) overrides the choice.
 int prefill_layout(int n_tiles, int B, bool ragged, int cus) {
   const int forced = launch_knob(BRAID_KNOB_PREFILL_LAYOUT);
-  if (forced == 1 || forced == 2 || forced == 4) return forced;
+  if (forced == 1 || forced == 2 || forced == 4 || forced == 8) return forced;
   if (forced == 0 && ragged && B <= kMaxPlanRows) return 0;
+  if (cus > 0 && 8 * n_tiles <= cus) return 8;
   if (cus > 0 && 4 * n_tiles <= cus) return 4;
   if (cus > 0 && 2 * n_tiles <= cus) return 1;
   return ragged && B <= kMaxPlanRows && cus > 0 && n_tiles <= 4 * cus ? 0 : 2;
@@ -1159,14 +1238,17 @@ int launch_prefill(void* pool, int pool_dtype, const int32_t* slot_idx, int B, i
   // the planned kernel's does not: config 4's 4 x 256 tokens 0.155 ms
   // planned, 0.132 ms in the split kernel).
   int host_plan = -1;
-  if (host_lens != nullptr && launch_knob(BRAID_KNOB_PREFILL_LAYOUT) < 0 &&
+  if (host_lens != nullptr && layout != 8 && launch_knob(BRAID_KNOB_PREFILL_LAYOUT) < 0 &&
       launch_knob(BRAID_KNOB_PREFILL_PLAN) < 0 && B <= kMaxPlanRows && cus > 0 &&
       B * H <= 4 * cus) {
     host_plan = host_prefill_plan(*host_lens, T, H, cus);
     const int n4 = host_plan >> 10, n2 = host_plan & 1023;
     layout = n4 == B ? 4 : (n2 == B ? 1 : 0);
   }
-  if (layout == 4)
+  if (layout == 8)
+    launch_prefill_cols<Gates, 8>(pool, pool_dtype, slot_idx, B, T, H, G, q, k, v, gates, y,
+                                  stream);
+  else if (layout == 4)
     launch_prefill_cols<Gates, 4>(pool, pool_dtype, slot_idx, B, T, H, G, q, k, v, gates, y,
                                   stream);
   else if (layout == 1)

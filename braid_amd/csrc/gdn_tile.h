@@ -744,8 +744,38 @@ struct ScanMapQuarter {
   __device__ __forceinline__ bool stores_y() const { return w == 0 && rgh == 0; }
 };
 
+// Eighth scan layout: one column and one row group per lane, so a lane holds
+// exactly one of the decode's eight-row chains (rows w * 32 + rg + 4 i) and a
+// tile spreads over eight workgroups of four waves (4 columns per wave).
+// Lane l: row group rg = l % 4, row block w = (l / 4) % 4, column cc = l / 16.
+// Column totals: the in-lane chain, then lane xor 1 and xor 2 give
+// (rg0 + rg1) + (rg2 + rg3), then xor 4 and xor 8 give (w0 + w1) + (w2 + w3):
+// the decode's order, every exchange inside a 16-lane row (DPP).
+struct ScanMapEighth {
+  static constexpr int kCPL = 1;
+  static constexpr int kLaneRowGroups = 1;
+  static constexpr int kColsPerWave = 4;
+  static constexpr int kWavesPerTile = kHD / kColsPerWave;
+  static constexpr int kWaves = 4;  // per workgroup
+  static constexpr int kParts = kWavesPerTile / kWaves;
+  int wave, lane, cc, rg, w, col0;
+  __device__ __forceinline__ ScanMapEighth(int tid, int part) {
+    lane = tid & 63;
+    wave = tid >> 6;
+    rg = lane & 3;
+    w = (lane >> 2) & 3;
+    cc = lane >> 4;
+    col0 = (part * kWaves + wave) * kColsPerWave + cc;
+  }
+  __device__ __forceinline__ int row(int i) const {
+    return w * kRowsPerWave + rg + kRowGroups * i;
+  }
+  __device__ __forceinline__ bool stores_y() const { return (lane & 15) == 0; }
+};
+
 // Scan layout of a prefill launch by code: 1 and 2 columns per lane
-// (ScanMap), 4 for the quarter layout (four workgroups per tile).
+// (ScanMap), 4 for the quarter layout (four workgroups per tile), 8 for the
+// eighth layout (eight).
 template <int L>
 struct ScanLayoutOf {
   using type = ScanMap<L>;
@@ -753,6 +783,10 @@ struct ScanLayoutOf {
 template <>
 struct ScanLayoutOf<4> {
   using type = ScanMapQuarter;
+};
+template <>
+struct ScanLayoutOf<8> {
+  using type = ScanMapEighth;
 };
 
 // Column total of the scan layout from a lane's four row-group chains:
@@ -1088,6 +1122,38 @@ __device__ __forceinline__ void scan_token_quarter(RowPair1<Tag> (&P)[kRowsPerLa
     for (int g = 0; g < 2; ++g) ch[g] = fmaf(n[g], qh[g][i], ch[g]);
   }
   y = add_xor32(add_xor16(add_xor8(ch[0] + ch[1]))) * kYScale;
+}
+
+// One token of the eighth layout on this lane's chain of 8 rows x 1 column:
+// P[m] holds rows i = 2m (low half) and 2m + 1 (high half) of the chain
+// (row w * 32 + rg + 4 i); kh / qh hold the same rows. Each element's
+// operations are scan_token's (and so the decode's), in the same order; the
+// column totals follow the layout's tree.
+template <class Tag, bool kOpaqueNarrow = false>
+__device__ __forceinline__ void scan_token_eighth(RowPair1<Tag> (&P)[kRowsPerLane / 2],
+                                                  const float (&kh)[kRowsPerLane],
+                                                  const float (&qh)[kRowsPerLane], float v,
+                                                  float alpha, float beta, float& y) {
+  const float nz = opaque(-0.0f);
+  float ch = first_term(P[0].get(0), kh[0], nz);
+#pragma unroll
+  for (int i = 1; i < kRowsPerLane; ++i) ch = fmaf(P[i >> 1].get(i & 1), kh[i], ch);
+  const float kv = add_xor8(add_xor4(add_xor2(add_xor1(ch))));
+  const float delta = (v - alpha * kv) * beta;
+  ch = 0.f;
+#pragma unroll
+  for (int m = 0; m < kRowsPerLane / 2; ++m) {
+    float n[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      n[h] = fmaf(alpha, P[m].get(h), kh[2 * m + h] * delta);
+      if constexpr (kOpaqueNarrow) n[h] = opaque(n[h]);
+    }
+    P[m].set(n[0], n[1]);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) ch = fmaf(n[h], qh[2 * m + h], ch);
+  }
+  y = add_xor8(add_xor4(add_xor2(add_xor1(ch)))) * kYScale;
 }
 
 // Computes one token's gates once per tile and leaves them in lds.gate for

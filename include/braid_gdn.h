@@ -59,7 +59,7 @@ const char* braid_last_error(void);
  *
  *   BRAID_KNOB_DECODE_XCD_REMAP  (BRAID_DECODE_XCD_REMAP)  0 / 1
  *   BRAID_KNOB_DECODE_WGS_PER_CU (BRAID_DECODE_WGS_PER_CU) 0 uncapped, N
- *   BRAID_KNOB_PREFILL_LAYOUT    (BRAID_PREFILL_COLS)      1, 2, 4, or 0 planned
+ *   BRAID_KNOB_PREFILL_LAYOUT    (BRAID_PREFILL_COLS)      1, 2, 4, 8, or 0 planned
  *   BRAID_KNOB_DECODE_PARTS      (BRAID_DECODE_PARTS)      1, 2 or 4 column parts
  *   BRAID_KNOB_PREFILL_PLAN      (BRAID_PREFILL_PLAN)      n4 * 1024 + n2: a planned
  *                                prefill runs its n4 longest rows in the quarter

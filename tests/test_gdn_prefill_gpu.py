@@ -291,16 +291,16 @@ def test_identity_steps_are_exact_up_to_the_sign_of_zero(kern, dt):
     assert torch.equal(pr, pd) and _same_up_to_zero_sign(pr, pd, dt)
 
 
-@pytest.mark.parametrize("cols", [1, 2, 0, 4],
-                         ids=["split-1col", "whole-2col", "planned", "quarter"])
+@pytest.mark.parametrize("cols", [1, 2, 0, 4, 8],
+                         ids=["split-1col", "whole-2col", "planned", "quarter", "eighth"])
 @pytest.mark.parametrize("dt", POOL_DTYPES, ids=POOL_IDS)
 def test_both_scan_layouts_are_decode_bit_for_bit(kern, dt, cols):
     """The launch picks one column per lane (a tile split over two workgroups)
     for small launches, two otherwise, or, for larger ragged batches, a plan
-    per row; the quarter layout (one column and 16 rows per lane, a tile over
-    four workgroups) serves the smallest launches (the prefill_layout knob
-    = 1, 2, 0 or 4 forces each; here the planned launch splits the 40-token row and
-    runs the others whole). Every layout
+    per row; the quarter and eighth layouts (one column and 16 or 8 rows per
+    lane, a tile over four or eight workgroups) serve the smallest launches
+    (the prefill_layout knob = 1, 2, 0, 4 or 8 forces each; here the planned
+    launch splits the 40-token row and runs the others whole). Every layout
     must equal decode applied T times, with raw gates and ragged seq_lens
     including 0, on every pool type, with zeros at the pad outputs."""
     B, T, H, G = 3, 40, 32, 16
