@@ -440,11 +440,16 @@ def measure_paths(torch, kern):
             t_plan = time.perf_counter()
             plan = kern._lib.braid_prefill_plan(host.ctypes.data, Bp, T, H, cus)
             plan_times.append(time.perf_counter() - t_plan)
-        n4, n2 = plan >> 10, plan & 1023
-        # the launch an eager call makes: one tier for every row runs that
-        # layout's own kernel, otherwise the planned kernel with this plan
-        knobs = ({"prefill_layout": 4} if n4 == Bp else {"prefill_layout": 1} if n2 == Bp
-                 else {"prefill_layout": 0, "prefill_plan": plan})
+        n8, n4, n2 = plan >> 20, (plan >> 10) & 1023, plan & 1023
+        # the launch an eager call makes: a launch small enough for the eighth
+        # layout runs it without planning; one tier for every row runs that
+        # layout's own kernel; otherwise the planned kernel with this plan
+        if 8 * Bp * H <= cus:
+            knobs, n8, n4, n2 = {}, Bp, 0, 0
+        else:
+            knobs = ({"prefill_layout": 8} if n8 == Bp else {"prefill_layout": 4} if n4 == Bp
+                     else {"prefill_layout": 1} if n2 == Bp
+                     else {"prefill_layout": 0, "prefill_plan": plan})
         with kern.launch_override(**knobs):
             t = graph_time(torch, call, reps=11)
         t_dev = graph_time(torch, call, reps=11)
@@ -453,7 +458,7 @@ def measure_paths(torch, kern):
         return {"rows": Bp, "max_T": T, "tokens": tok, "ms": round(t * 1e3, 3),
                 "tokens_per_s": round(tok / t, 1), "tflops": round(tf, 2),
                 "fp32_frac": round(tf / FP32_PEAK_TFLOPS, 4),
-                "plan": {"quarter_rows": plan >> 10, "split_rows": plan & 1023},
+                "plan": {"eighth_rows": n8, "quarter_rows": n4, "split_rows": n2},
                 "host_plan_us": round(min(plan_times) * 1e6, 1),
                 "captured_kernel_plan_ms": round(t_dev * 1e3, 3)}
 
@@ -493,8 +498,8 @@ def measure_paths(torch, kern):
 
     lens = torch.randint(64, 1025, (8,), generator=torch.Generator().manual_seed(2)).tolist()
     out["prefill_config2"] = prefill_case(lens)
-    # the small-batch regime: one 512-token row (quarter layout, four workgroups
-    # per tile) and one 1024-token row among 15 of 128 (the plan runs it quarter)
+    # the small-batch regime: one 512-token row (eighth layout, eight workgroups
+    # per tile) and one 1024-token row among 15 of 128 (planned)
     out["prefill_one_row_512"] = prefill_case([512])
     out["prefill_skewed_1x1024_15x128"] = prefill_case([1024] + [128] * 15)
 

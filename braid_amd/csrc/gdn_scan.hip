@@ -788,7 +788,7 @@ gdn_prefill_planned_kernel(typename Storage<Tag>::T* __restrict__ pool,
   __shared__ StageLds st;
   __shared__ int lens[kMaxPlanRows];
   __shared__ int order[kMaxPlanRows];  // row of each rank
-  __shared__ int plan[2];  // n4, n2
+  __shared__ int plan[3];  // n4, n2, n8
   for (int r = threadIdx.x; r < B; r += blockDim.x) lens[r] = gates.row_len(r, T);
   __syncthreads();
   for (int r = threadIdx.x; r < B; r += blockDim.x) {
@@ -835,18 +835,30 @@ gdn_prefill_planned_kernel(typename Storage<Tag>::T* __restrict__ pool,
     }
     plan[0] = b4;
     plan[1] = b2;
-    // A plan forced for measurement (n4 * 1024 + n2; the launch sized the
-    // grid for it).
+    plan[2] = 0;
+    // A plan chosen on the host or forced for measurement (n8 * 2^20 + n4 *
+    // 2^10 + n2; the launch sized the grid for it).
     if (forced_plan >= 0) {
-      plan[0] = min(forced_plan >> 10, B);
-      plan[1] = min(forced_plan & 1023, B - plan[0]);
+      plan[2] = min(forced_plan >> 20, B);
+      plan[0] = min((forced_plan >> 10) & 1023, B - plan[2]);
+      plan[1] = min(forced_plan & 1023, B - plan[2] - plan[0]);
     }
   }
   __syncthreads();
-  const int n4 = plan[0], n2 = plan[1];
+  const int n4 = plan[0], n2 = plan[1], n8 = plan[2];
   int i = blockIdx.x;
+  // Ranks: the n8 longest rows in the eighth layout, the next n4 quarter,
+  // then n2 split, the rest whole; workgroups in that order.
+  if (i < 8 * n8 * H) {
+    const int rank = i / (8 * H), rem = i - rank * 8 * H;
+    const int b = order[rank];
+    prefill_tile<Tag, Gates, 8, true>(pool, slot_idx, q, k, v, gates, y, H, G, heads_per_group, T,
+                                      b, rem >> 3, rem & 7, lens[b], st);
+    return;
+  }
+  i -= 8 * n8 * H;
   if (i < 4 * n4 * H) {
-    const int rank = i / (4 * H), rem = i - rank * 4 * H;
+    const int rank = n8 + i / (4 * H), rem = i - (rank - n8) * 4 * H;
     const int b = order[rank];
     prefill_tile<Tag, Gates, 4, true>(pool, slot_idx, q, k, v, gates, y, H, G, heads_per_group, T,
                                       b, rem >> 2, rem & 3, lens[b], st);
@@ -854,15 +866,15 @@ gdn_prefill_planned_kernel(typename Storage<Tag>::T* __restrict__ pool,
   }
   i -= 4 * n4 * H;
   if (i < 2 * n2 * H) {
-    const int rank = n4 + i / (2 * H), rem = i - (rank - n4) * 2 * H;
+    const int rank = n8 + n4 + i / (2 * H), rem = i - (rank - n8 - n4) * 2 * H;
     const int b = order[rank];
     prefill_tile<Tag, Gates, 1>(pool, slot_idx, q, k, v, gates, y, H, G, heads_per_group, T, b,
                                 rem >> 1, rem & 1, lens[b], st);
     return;
   }
   i -= 2 * n2 * H;
-  if (i < (B - n4 - n2) * H) {
-    const int rank = n4 + n2 + i / H;
+  if (i < (B - n8 - n4 - n2) * H) {
+    const int rank = n8 + n4 + n2 + i / H;
     const int b = order[rank];
     prefill_tile<Tag, Gates, 2>(pool, slot_idx, q, k, v, gates, y, H, G, heads_per_group, T, b,
                                 i - (i / H) * H, 0, lens[b], st);
@@ -1047,12 +1059,13 @@ void launch_prefill_planned(void* pool, int pool_dtype, const int32_t* slot_idx,
   // At most one extra workgroup per CU for split tiles; the grid has room for
   // whatever the plan uses (the rest return at once).
   const int max_extra = std::min(cus, 3 * B * H);
-  // forced: a plan chosen on the host (n4 * 1024 + n2), or -1 for the
+  // forced: a plan chosen on the host (n8 * 2^20 + n4 * 2^10 + n2), or -1 for the
   // kernel's own; the grid holds whichever plan runs.
   int n_wg = B * H + max_extra;
   if (forced >= 0) {
-    const int n4 = std::min(forced >> 10, B), n2 = std::min(forced & 1023, B - n4);
-    n_wg = std::max(n_wg, (4 * n4 + 2 * n2 + (B - n4 - n2)) * H);
+    const int n8 = std::min(forced >> 20, B), n4 = std::min((forced >> 10) & 1023, B - n8);
+    const int n2 = std::min(forced & 1023, B - n8 - n4);
+    n_wg = std::max(n_wg, (8 * n8 + 4 * n4 + 2 * n2 + (B - n8 - n4 - n2)) * H);
   }
   const dim3 grid((unsigned)n_wg), block(256);
   const int hpg = H / G;
@@ -1085,17 +1098,21 @@ void launch_prefill_planned(void* pool, int pool_dtype, const int32_t* slot_idx,
 // row's tokens at a per-token cost of its tier, solo or sharing its CU, and
 // the cost changes whenever its partner starts or ends. CUs with the same
 // contents form one class, so a simulation is a few dozen events. The costs,
-// relative, were fitted on MI355X to every plan (n4 <= 6, n2 <= 8) timed over
-// 11 ragged batches (fp16 pool, H = 32), per token: quarter 0.344 solo /
-// 0.451 shared, split 0.389 / 0.46, whole 0.606 / 0.978. Against the best
-// measured plan of each batch the chosen ones are 10% slower in sum over the
-// 11 (at most 5.6%, on one 1024-token row among 15 of 128); the kernel's own
+// relative, were fitted on MI355X to every plan (n8 <= 2, n4 <= 6, n2 <= 8)
+// timed over 11 ragged batches (fp16 pool, H = 32), per token: eighth 0.268
+// solo / 0.308 shared, quarter 0.344 / 0.469, split 0.416 / 0.499, whole
+// 0.619 / 0.871. Against the best measured plan of each batch the chosen ones
+// are 6.4% slower in sum over the 11 (at most 4.3%; config 2's is its best,
+// 0.426 ms); the kernel's own
 // estimate had chosen plans up to 35% slower (config 2: 0.538 against 0.474
 // ms; 4 rows of ~1000 and ~300 tokens: 0.484 against 0.359 ms).
 struct TierCost {
   float solo, shared;
 };
-constexpr TierCost kPlanCost[3] = {{0.344f, 0.451f}, {0.389f, 0.46f}, {0.606f, 0.978f}};
+// Tiers: 0 eighth, 1 quarter, 2 split, 3 whole.
+constexpr TierCost kPlanCost[4] = {
+    {0.268f, 0.308f}, {0.344f, 0.469f}, {0.416f, 0.499f}, {0.619f, 0.871f}};
+constexpr int kTierParts[4] = {8, 4, 2, 1};
 
 struct PlanJob {
   float rem, solo, shared;  // fraction of the job left; its duration solo / shared
@@ -1138,16 +1155,16 @@ struct PlanSim {
     }
   }
 
-  float makespan(const std::vector<int>& sorted_lens, int n4, int n2, int H, int cus) {
+  float makespan(const std::vector<int>& sorted_lens, int n8, int n4, int n2, int H, int cus) {
     const int B = (int)sorted_lens.size();
     rows.clear();
     qi = 0;
     for (int r = 0; r < B; ++r) {
-      const int tier = r < n4 ? 0 : (r < n4 + n2 ? 1 : 2);
+      const int tier = r < n8 ? 0 : (r < n8 + n4 ? 1 : (r < n8 + n4 + n2 ? 2 : 3));
       const float L = (float)sorted_lens[r];
       if (sorted_lens[r] > 0)
-        rows.push_back({(long)(tier == 0 ? 4 : tier == 1 ? 2 : 1) * H,
-                        kPlanCost[tier].solo * L, kPlanCost[tier].shared * L});
+        rows.push_back({(long)kTierParts[tier] * H, kPlanCost[tier].solo * L,
+                        kPlanCost[tier].shared * L});
     }
     next.clear();
     cls.clear();
@@ -1191,11 +1208,12 @@ struct PlanSim {
   }
 };
 
-// The plan (n4 * 1024 + n2) with the least simulated makespan, over n4 <= 6
-// quarter rows and n2 <= 8 split rows (ties: the first found, fewer
-// upgraded rows). A candidate is not simulated when a lower bound already
-// reaches the best plan so far: its longest row in each tier alone and
-// solo, or all its work spread over every slot at the shared costs.
+// The plan (n8 * 2^20 + n4 * 2^10 + n2) with the least simulated makespan,
+// over n8 <= 2 eighth rows, n4 <= 6 quarter rows and n2 <= 8 split rows
+// (ties: the first found, fewer upgraded rows). A candidate is not simulated
+// when a lower bound already reaches the best plan so far: its longest row
+// in each tier alone and solo, or all its work spread over every slot at the
+// shared costs.
 int host_prefill_plan(const std::vector<int32_t>& seq_lens, int T, int H, int cus) {
   std::vector<int> lens(seq_lens.size());
   for (size_t r = 0; r < lens.size(); ++r) lens[r] = std::min(std::max((int)seq_lens[r], 0), T);
@@ -1206,23 +1224,27 @@ int host_prefill_plan(const std::vector<int32_t>& seq_lens, int T, int H, int cu
   PlanSim sim;
   float best = INFINITY;
   int plan = 0;
-  for (int n4 = 0; n4 <= std::min(B, 6); ++n4)
-    for (int n2 = 0; n2 <= std::min(B - n4, 8); ++n2) {
-      float bound = 0.f;
-      if (n4 > 0) bound = std::max(bound, kPlanCost[0].solo * lens[0]);
-      if (n2 > 0) bound = std::max(bound, kPlanCost[1].solo * lens[n4]);
-      if (n4 + n2 < B) bound = std::max(bound, kPlanCost[2].solo * lens[n4 + n2]);
-      const double work = H * (4.0 * kPlanCost[0].shared * prefix[n4] +
-                               2.0 * kPlanCost[1].shared * (prefix[n4 + n2] - prefix[n4]) +
-                               kPlanCost[2].shared * (prefix[B] - prefix[n4 + n2]));
-      bound = std::max(bound, (float)(work / (2.0 * cus)));
-      if (bound >= best) continue;
-      const float m = sim.makespan(lens, n4, n2, H, cus);
-      if (m < best) {
-        best = m;
-        plan = n4 * 1024 + n2;
+  for (int n8 = 0; n8 <= std::min(B, 2); ++n8)
+    for (int n4 = 0; n4 <= std::min(B - n8, 6); ++n4)
+      for (int n2 = 0; n2 <= std::min(B - n8 - n4, 8); ++n2) {
+        const int first[4] = {0, n8, n8 + n4, n8 + n4 + n2};
+        const int count[4] = {n8, n4, n2, B - n8 - n4 - n2};
+        float bound = 0.f;
+        double work = 0.0;
+        for (int t = 0; t < 4; ++t) {
+          if (count[t] == 0) continue;
+          bound = std::max(bound, kPlanCost[t].solo * lens[first[t]]);
+          work += kTierParts[t] * kPlanCost[t].shared *
+                  (prefix[first[t] + count[t]] - prefix[first[t]]);
+        }
+        bound = std::max(bound, (float)(H * work / (2.0 * cus)));
+        if (bound >= best) continue;
+        const float m = sim.makespan(lens, n8, n4, n2, H, cus);
+        if (m < best) {
+          best = m;
+          plan = (n8 << 20) | (n4 << 10) | n2;
+        }
       }
-    }
   return plan;
 }
 
@@ -1242,8 +1264,8 @@ int launch_prefill(void* pool, int pool_dtype, const int32_t* slot_idx, int B, i
       launch_knob(BRAID_KNOB_PREFILL_PLAN) < 0 && B <= kMaxPlanRows && cus > 0 &&
       B * H <= 4 * cus) {
     host_plan = host_prefill_plan(*host_lens, T, H, cus);
-    const int n4 = host_plan >> 10, n2 = host_plan & 1023;
-    layout = n4 == B ? 4 : (n2 == B ? 1 : 0);
+    const int n8 = host_plan >> 20, n4 = (host_plan >> 10) & 1023, n2 = host_plan & 1023;
+    layout = n8 == B ? 8 : (n4 == B ? 4 : (n2 == B ? 1 : 0));
   }
   if (layout == 8)
     launch_prefill_cols<Gates, 8>(pool, pool_dtype, slot_idx, B, T, H, G, q, k, v, gates, y,

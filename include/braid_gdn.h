@@ -61,9 +61,10 @@ const char* braid_last_error(void);
  *   BRAID_KNOB_DECODE_WGS_PER_CU (BRAID_DECODE_WGS_PER_CU) 0 uncapped, N
  *   BRAID_KNOB_PREFILL_LAYOUT    (BRAID_PREFILL_COLS)      1, 2, 4, 8, or 0 planned
  *   BRAID_KNOB_DECODE_PARTS      (BRAID_DECODE_PARTS)      1, 2 or 4 column parts
- *   BRAID_KNOB_PREFILL_PLAN      (BRAID_PREFILL_PLAN)      n4 * 1024 + n2: a planned
- *                                prefill runs its n4 longest rows in the quarter
- *                                layout and the next n2 split
+ *   BRAID_KNOB_PREFILL_PLAN      (BRAID_PREFILL_PLAN)      n8 * 2^20 + n4 * 2^10 + n2:
+ *                                a planned prefill runs its n8 longest rows in the
+ *                                eighth layout, the next n4 quarter, the next n2
+ *                                split
  *
  * A captured graph keeps the launch shape it was captured with.
  */
@@ -76,10 +77,11 @@ enum braid_launch_knob {
 };
 /*
  * The plan an eager braid_gdn_prefill_raw with seq_lens chooses for a ragged
- * batch: n4 * 1024 + n2 (its n4 longest rows in the quarter layout, the next
- * n2 split over two workgroups, the rest whole), from host lengths, for `cus`
- * CUs; -BRAID_EINVAL on bad arguments. Host-only (no GPU call), for
- * measurement and tests. No counterpart in the reference.
+ * batch: n8 * 2^20 + n4 * 2^10 + n2 (its n8 longest rows in the eighth layout,
+ * eight workgroups per tile; the next n4 quarter, four; the next n2 split
+ * over two; the rest whole), from host lengths, for `cus` CUs; -BRAID_EINVAL
+ * on bad arguments. Host-only (no GPU call), for measurement and tests. No
+ * counterpart in the reference.
  */
 int braid_prefill_plan(const int32_t* seq_lens_host, int B, int T, int H, int cus);
 

@@ -179,25 +179,27 @@ def test_stream_probe_library_loads_and_rejects_bad_arguments():
 
 
 def test_host_prefill_plan_picks_the_measured_plans(lib):
-    """braid_prefill_plan: the tiers an eager ragged prefill runs (n4 quarter
-    rows, n2 split rows; returned as n4 * 1024 + n2), chosen by simulating the
+    """braid_prefill_plan: the tiers an eager ragged prefill runs (n8 eighth
+    rows, n4 quarter rows, n2 split rows; returned as n8 * 2^20 + n4 * 2^10 +
+    n2), chosen by simulating the
     launch on 256 CUs of two workgroup slots. The expected plans are the
     choices that measured within a few percent of the best of every plan
     timed on MI355X (H = 32); they pin the simulation, the cost table and the
     tie order."""
     cases = {
-        (454, 610, 334, 542, 393, 861, 814, 65): (1, 5),   # config 2
-        (1003, 300, 1001, 383): (3, 1),
-        (900, 850, 200, 200, 200, 200, 200, 200): (2, 2),
-        (256,) * 16: (0, 0),
+        (454, 610, 334, 542, 393, 861, 814, 65): (0, 1, 6),   # config 2
+        (1003, 300, 1001, 383): (0, 3, 1),
+        (900, 850, 200, 200, 200, 200, 200, 200): (0, 2, 2),
+        (1024,) + (128,) * 15: (1, 0, 0),
+        (256,) * 16: (0, 0, 0),
     }
-    for lens, (n4, n2) in cases.items():
+    for lens, plan in cases.items():
         arr = (ctypes.c_int32 * len(lens))(*lens)
         p = lib.braid_prefill_plan(arr, len(lens), max(lens), 32, 256)
-        assert (p >> 10, p & 1023) == (n4, n2), lens
-    # one row: all quarter would be the fastest layout; a batch of empty rows plans nothing
+        assert (p >> 20, (p >> 10) & 1023, p & 1023) == plan, lens
+    # one row: the eighth layout; a batch of empty rows plans nothing
     one = (ctypes.c_int32 * 1)(700)
-    assert lib.braid_prefill_plan(one, 1, 700, 32, 256) >> 10 == 1
+    assert lib.braid_prefill_plan(one, 1, 700, 32, 256) == 1 << 20
     zeros = (ctypes.c_int32 * 3)(0, 0, 0)
     assert lib.braid_prefill_plan(zeros, 3, 10, 32, 256) == 0
     assert lib.braid_prefill_plan(None, 3, 10, 32, 256) == -1

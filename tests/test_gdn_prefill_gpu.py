@@ -330,6 +330,37 @@ def test_both_scan_layouts_are_decode_bit_for_bit(kern, dt, cols):
     assert bool(same.all()), f"states differ by {(pc.float() - ps.float()).abs().max().item():.3e}"
 
 
+@pytest.mark.parametrize("dt", POOL_DTYPES, ids=POOL_IDS)
+def test_a_plan_with_every_tier_is_decode_bit_for_bit(kern, dt):
+    """A planned launch forced to use all four tiers (the longest row in the
+    eighth layout, the next quarter, the next split, the rest whole; the
+    prefill_plan knob, n8 * 2^20 + n4 * 2^10 + n2) equals decode applied token
+    by token, bit for bit, with zeros at the pad outputs."""
+    lens_l = [37, 29, 18, 11, 0]
+    B, T, H, G = len(lens_l), max(lens_l), 32, 16
+    inp = prefill_inputs(B, T, H=H, G=G, seed=81)
+    a, b, A, dtb = raw_gates((B, T, H), H, torch.bfloat16, seed=82)
+    lens = torch.tensor(lens_l, dtype=torch.int32, device=DEV)
+    slots = torch.tensor([6, 2, 0, 4, 1], dtype=torch.int32, device=DEV)
+    pc = pool(8, H=H, dtype=dt)
+    ps = pc.clone()
+    yc = torch.empty(B, T, H, 128, device=DEV)
+    with kern.launch_override(prefill_layout=0, prefill_plan=(1 << 20) | (1 << 10) | 1):
+        kern.gdn_prefill_raw(pc, slots, inp["q"], inp["k"], inp["v"], a, b, A, dtb, yc, lens)
+    for t in range(T):
+        live = (t < lens).nonzero().flatten()
+        yt = torch.empty(live.numel(), H, 128, device=DEV)
+        kern.gdn_decode_raw(ps, slots[live].contiguous(), inp["q"][live, t].contiguous(),
+                            inp["k"][live, t].contiguous(), inp["v"][live, t].contiguous(),
+                            a[live, t].contiguous(), b[live, t].contiguous(), A, dtb, yt)
+        assert torch.equal(yc[live, t], yt), f"token {t}: outputs differ"
+        dead = (t >= lens).nonzero().flatten()
+        assert bool((yc[dead, t] == 0).all()), f"token {t}: pad outputs are not 0"
+    torch.cuda.synchronize()
+    same = (pc == ps) | (pc.isnan() & ps.isnan())
+    assert bool(same.all()), f"states differ by {(pc.float() - ps.float()).abs().max().item():.3e}"
+
+
 def test_a_skewed_ragged_batch_is_decode_bit_for_bit(kern):
     """One long row among short ones: the default launch plans the long row's
     tiles in the quarter layout (its chain, not the total work, bounds the
