@@ -242,13 +242,17 @@ def copy_bandwidth(torch, nbytes=2 ** 30):
     return 2 * nbytes / secs / 1e9
 
 
-def stream_ceiling(torch, n_pools, launches=256):
+def stream_ceiling(torch, n_pools, launches=256, order="row_major"):
     """What an in-place stream of the step's state tiles reaches on this box:
     libbraid_probe.so's read-modify-write, read-only and write-only passes
     over the same 4096 tiles of 32 KiB (slot-permuted, cold pools, the
     decode's lane layout, nontemporal 128-bit accesses), without the
-    arithmetic or the q/k/v/y traffic. Captured in one graph, timed with
-    events. GB/s count the state bytes each pass moves."""
+    arithmetic or the q/k/v/y traffic. Captured in one graph, timed on the
+    GPU clock. GB/s count the state bytes each pass moves.
+
+    `order` is the order the launch visits the same tiles in: "row_major" is
+    the decode's (row b's 32 heads are consecutive tiles); "head_major" puts
+    head h of every row together; "shuffled" is a seeded random order."""
     import ctypes
 
     from braid_amd.build import PROBE_LIB
@@ -266,8 +270,14 @@ def stream_ceiling(torch, n_pools, launches=256):
     maps = []
     for p in range(n_pools):
         perm = torch.randperm(SLOTS, generator=torch.Generator().manual_seed(p))[:B]
-        maps.append((perm[:, None] * H + torch.arange(H)[None, :]).reshape(-1)
-                    .to(torch.int32).to(dev))
+        tiles = perm[:, None] * H + torch.arange(H)[None, :]
+        if order == "head_major":
+            tiles = tiles.t()
+        tiles = tiles.reshape(-1)
+        if order == "shuffled":
+            tiles = tiles[torch.randperm(tiles.numel(),
+                                         generator=torch.Generator().manual_seed(100 + p))]
+        maps.append(tiles.to(torch.int32).to(dev))
     sink = torch.empty(1024, dtype=torch.int32, device=dev)
     n_tiles = B * H
     tile_bytes = D * D * 2
@@ -607,11 +617,37 @@ def measure_paths(torch, kern):
                                      ly["bias"], ly["a"], ly["b"], A, dtb, ly["y"], G)
 
     t_fused = graph_time(torch, mixer_step_fused, reps=11)
+
+    # The step's parts, each as its own 24-launch sequence, and the dispatch
+    # floor: 24 one-thread kernels (braid_probe_clock) in the same kind of
+    # graph. A dependent launch costs about that much even when it does nothing.
+    def quant_only():
+        for ly in layers:
+            kern.quantize_act(ly["x"])
+
+    def fused_only():
+        for ly in layers:
+            kern.gdn_conv_decode_raw(ly["pool"], ly["conv"], slots64, ly["xin"], ly["w"],
+                                     ly["bias"], ly["a"], ly["b"], A, dtb, ly["y"], G)
+
+    floor_clock = GpuClock(torch)
+    floor_buf = torch.zeros(L, dtype=torch.int64, device=dev)
+
+    def empty_launches():
+        st = torch.cuda.current_stream().cuda_stream
+        for i in range(L):
+            floor_clock._stamp(floor_buf[i:].data_ptr(), st)
+
+    parts = {"quantize_act_us": round(graph_time(torch, quant_only, reps=11) * 1e6, 1),
+             "conv_decode_us": round(graph_time(torch, fused_only, reps=11) * 1e6, 1),
+             "dispatch_floor_us_per_launch":
+                 round(graph_time(torch, empty_launches, reps=11) / L * 1e6, 2)}
     out["mixer_step_fused"] = {"layers": L, "batch": Bm, "us": round(t_fused * 1e6, 1),
                                "gbs": round(step_bytes / t_fused / 1e9, 1),
                                "hbm_frac": round(step_bytes / t_fused / 1e9 / HBM_PEAK_GBS, 4),
                                "note": "conv + decode in one launch per layer; same bytes "
-                                       "credited as mixer_step"}
+                                       "credited as mixer_step",
+                               "parts_24_layers": parts}
     out["mixer_step"] = {"layers": L, "batch": Bm, "us": round(t * 1e6, 1),
                          "gbs": round(step_bytes / t / 1e9, 1),
                          "hbm_frac": round(step_bytes / t / 1e9 / HBM_PEAK_GBS, 4),
@@ -693,6 +729,8 @@ def main():
     torch.cuda.empty_cache()
     copy_gbs = copy_bandwidth(torch)
     ceiling = stream_ceiling(torch, n_cold)
+    orders = {o: stream_ceiling(torch, n_cold, launches=64, order=o)
+              for o in ("head_major", "shuffled")}
     torch.cuda.empty_cache()
 
     step_s = t_cold / args.steps
@@ -737,6 +775,8 @@ def main():
         # (libbraid_probe.so); decode_vs_rmw = probe time / decode time
         "stream_ceiling": dict(ceiling, decode_vs_rmw=round(ceiling["rmw_us"] / (step_s * 1e6),
                                                             4)),
+        # the same probe passes over the same tiles visited in other orders
+        "stream_ceiling_other_orders": orders,
     }
     if not args.no_paths:
         out["paths"] = measure_paths(torch, kern)
