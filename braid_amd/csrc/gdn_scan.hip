@@ -642,23 +642,40 @@ __device__ __forceinline__ void prefill_tile(typename Storage<Tag>::T* __restric
     const size_t y_tok = (size_t)H * kHD;
     int j = 0;
     if constexpr (Layout == 8) {
-      for (; j + 1 < n; j += 2) {
-        TokenInE in0, in1;
-        read_token_eighth(st, j, r0, L.col0, in0);
-        read_token_eighth(st, j + 1, r0, L.col0, in1);
+      // The next pair's inputs are read from the stage while this pair runs
+      // (the layout runs one wave per SIMD, so the 36 registers are free).
+      // Two pairs per iteration, so the buffers trade roles without copies;
+      // reads past the stage's live tokens stay inside it and go unused.
+      auto clamp = [](int t) { return min(t, kStage - 1); };
+      auto pair = [&](int jj, const TokenInE& a, const TokenInE& c) {
         float y0[1], y1[1];
-        scan_token_eighth<Tag, true>(S.p, in0.kh, in0.qh, in0.v, in0.alpha, in0.beta, y0[0]);
-        scan_token_eighth<Tag, true>(S.p, in1.kh, in1.qh, in1.v, in1.alpha, in1.beta, y1[0]);
+        scan_token_eighth<Tag, true>(S.p, a.kh, a.qh, a.v, a.alpha, a.beta, y0[0]);
+        scan_token_eighth<Tag, true>(S.p, c.kh, c.qh, c.v, c.alpha, c.beta, y1[0]);
         if (L.stores_y()) {
-          storeN<1>(yt + j * y_tok, y0);
-          storeN<1>(yt + (j + 1) * y_tok, y1);
+          storeN<1>(yt + jj * y_tok, y0);
+          storeN<1>(yt + (jj + 1) * y_tok, y1);
         }
+      };
+      TokenInE c0, c1, n0, n1;
+      read_token_eighth(st, 0, r0, L.col0, c0);
+      read_token_eighth(st, 1, r0, L.col0, c1);
+      for (; j + 3 < n; j += 4) {
+        read_token_eighth(st, j + 2, r0, L.col0, n0);
+        read_token_eighth(st, j + 3, r0, L.col0, n1);
+        pair(j, c0, c1);
+        read_token_eighth(st, clamp(j + 4), r0, L.col0, c0);
+        read_token_eighth(st, clamp(j + 5), r0, L.col0, c1);
+        pair(j + 2, n0, n1);
       }
-      for (; j < n; ++j) {
-        TokenInE in;
-        read_token_eighth(st, j, r0, L.col0, in);
+      if (j + 1 < n) {
+        read_token_eighth(st, clamp(j + 2), r0, L.col0, n0);
+        pair(j, c0, c1);
+        c0 = n0;
+        j += 2;
+      }
+      if (j < n) {
         float yy[1];
-        scan_token_eighth<Tag>(S.p, in.kh, in.qh, in.v, in.alpha, in.beta, yy[0]);
+        scan_token_eighth<Tag>(S.p, c0.kh, c0.qh, c0.v, c0.alpha, c0.beta, yy[0]);
         if (L.stores_y()) storeN<1>(yt + j * y_tok, yy);
       }
     } else if constexpr (Layout == 4) {
