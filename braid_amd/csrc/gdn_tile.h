@@ -329,12 +329,12 @@ __device__ __forceinline__ float dpp(float v) {
 __device__ __forceinline__ float add_xor1(float v) { return v + dpp<0xB1>(v); }
 __device__ __forceinline__ float add_xor2(float v) { return v + dpp<0x4E>(v); }
 
-// v + (v of lane xor 4): a lane with bit 2 clear reads lane + 4 (DPP
-// row_shl:4), one with bit 2 set reads lane - 4 (row_shr:4); both stay inside
-// the lane's 16-lane row.
+// v + (v of lane xor 4): DPP row_half_mirror gives t[i] = v[7 - i] within each
+// 8-lane half row, then quad_perm [3,2,1,0] reads t[4q + 3 - j] at lane
+// i = 4q + j, which is v[4 (1 - q) + j] = v[i xor 4]. Two DPP instructions,
+// the second fused into the add.
 __device__ __forceinline__ float add_xor4(float v) {
-  const float up = dpp<0x104>(v), down = dpp<0x114>(v);
-  return v + ((__lane_id() & 4) ? down : up);
+  return v + dpp<0x1B>(dpp<0x141>(v));
 }
 
 // v + (v of lane xor 8): DPP row_ror:8 (within each 16-lane row, rotating by
