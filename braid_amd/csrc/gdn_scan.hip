@@ -98,7 +98,7 @@ gdn_decode_kernel(typename Storage<Tag>::T* __restrict__ pool, const int* __rest
   normalize_qk_lds(L, q2, k2, qk_lds[L.wave], qk);
 
   float yy[CPL];
-  gdn_token<Tag, CPL>(L, S, qk, vv, lds, yy);
+  gdn_token<Tag, CPL, true>(L, S, qk, vv, lds, yy);
 
 #pragma unroll
   for (int i = 0; i < kRowsPerLane; ++i) store_row(S[i], L, tile + (size_t)L.row(i) * kHD);

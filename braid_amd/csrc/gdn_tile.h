@@ -361,8 +361,14 @@ __device__ __forceinline__ float wave_sum(float v) {
   return add_xor32(add_xor16(add_xor8(add_xor4(add_xor2(add_xor1(v))))));
 }
 
-// Sum over a wave's four row groups sharing a column chunk (lane bits 4, 5).
+// Sum over a wave's four row groups sharing a column chunk (lane bits 4, 5):
+// v + (lane xor 16), then + (lane xor 32). kPermlane: through the permlane
+// swaps (VALU); otherwise through ds_bpermute, which holds no extra registers
+// (the fused conv + decode kernels have none to spare at 128 VGPRs). Same
+// sums either way (a + b == b + a), so the same bits.
+template <bool kPermlane = false>
 __device__ __forceinline__ float rowgroup_sum(float v) {
+  if constexpr (kPermlane) return add_xor32(add_xor16(v));
   v += __shfl_xor(v, 16, 64);
   v += __shfl_xor(v, 32, 64);
   return v;
@@ -904,11 +910,11 @@ __device__ __forceinline__ void normalize_qk(const LM& L, const float* __restric
 //   column_sums_take:  after the barrier, read the four row blocks' partials
 //                      and add them by the fixed tree (w0 + w1) + (w2 + w3).
 // Every lane ends with the totals of its columns.
-template <int CPL, bool S>
+template <bool kPermlane = false, int CPL, bool S>
 __device__ __forceinline__ void column_sums_post(const LaneMap<CPL, S>& L, float (&part)[CPL],
                                                  float (*buf)[kHD]) {
 #pragma unroll
-  for (int c = 0; c < CPL; ++c) part[c] = rowgroup_sum(part[c]);
+  for (int c = 0; c < CPL; ++c) part[c] = rowgroup_sum<kPermlane>(part[c]);
   if (L.rg == 0) store_cols(L, buf[L.w], part);
 }
 
@@ -969,19 +975,19 @@ __device__ __forceinline__ void update_state(Row<Tag, CPL> (&S)[kRowsPerLane], c
 // after the first barrier, so whoever writes them must do so before it
 // (publish_gates). Contains two workgroup barriers, so all waves of the tile
 // must call it together.
-template <class Tag, int CPL, bool kSplit>
+template <class Tag, int CPL, bool kPermlane = false, bool kSplit>
 __device__ __forceinline__ void gdn_token(const LaneMap<CPL, kSplit>& L,
                                           Row<Tag, CPL> (&S)[kRowsPerLane], const QK& qk,
                                           const float (&v)[CPL], TileLds& lds,
                                           float (&y)[CPL]) {
   float kv[CPL];
   kv_partials<Tag, CPL>(S, qk, kv);
-  column_sums_post(L, kv, lds.kv);
+  column_sums_post<kPermlane>(L, kv, lds.kv);
   __syncthreads();
   column_sums_take(L, kv, lds.kv);
   float acc[CPL];
   update_state<Tag, CPL>(S, qk, v, kv, lds.gate[0], lds.gate[1], acc);
-  column_sums_post(L, acc, lds.y);
+  column_sums_post<kPermlane>(L, acc, lds.y);
   __syncthreads();
   column_sums_take(L, acc, lds.y);
 #pragma unroll
