@@ -113,8 +113,12 @@ __device__ __forceinline__ void gated_unit(float (&c)[4], const float (&zf)[4], 
                                            float& m) {
   round4(ATag{}, c);
   float ss = (c[0] * c[0] + c[1] * c[1]) + (c[2] * c[2] + c[3] * c[3]);
-#pragma unroll
-  for (int s = 1; s < kLanesPerUnit; s <<= 1) ss += __shfl_xor(ss, s, 64);
+  static_assert(kLanesPerUnit == 32, "a unit's sum runs over lane bits 0-4");
+  ss += lane_xor<1>(ss);
+  ss += lane_xor<2>(ss);
+  ss += lane_xor<4>(ss);
+  ss += lane_xor<8>(ss);
+  ss += lane_xor<16>(ss);
   const float r = rsqrtf(ss * (1.0f / kUnit) + eps);  // mean: exact power-of-two scale
   float o[4];
 #pragma unroll

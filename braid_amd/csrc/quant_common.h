@@ -55,13 +55,50 @@ __device__ __forceinline__ void load_vec(Tag tag, const uint16_t* x, long i, flo
     o[j] = widen(tag, (uint16_t)((r[j >> 1] >> (16 * (j & 1))) & 0xffffu));
 }
 
+// The value v holds in lane (this lane xor S), S a power of two below 64,
+// exchanged on the VALU rather than through the LDS crossbar (a ds_bpermute
+// is an LDS round trip per stage): DPP inside a 16-lane row for S = 1, 2 and
+// 8 (quad_perm [1,0,3,2], [2,3,0,1], row_ror:8); for S = 4, row_half_mirror
+// (t[i] = v[7 - i] in each 8-lane half) then quad_perm [3,2,1,0], which reads
+// t[4q + 3 - j] = v[(4q + j) xor 4]; for S = 16 and 32 the permlane swap of v
+// with itself, after which the two results hold the lower and the upper
+// block's value in every lane.
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, 0xf, 0xf, true));
+}
+template <int S>
+__device__ __forceinline__ float lane_xor(float v) {
+  if constexpr (S == 1) {
+    return dpp_f<0xB1>(v);
+  } else if constexpr (S == 2) {
+    return dpp_f<0x4E>(v);
+  } else if constexpr (S == 4) {
+    return dpp_f<0x1B>(dpp_f<0x141>(v));
+  } else if constexpr (S == 8) {
+    return dpp_f<0x128>(v);
+  } else {
+    static_assert(S == 16 || S == 32, "a lane-index bit");
+    const uint32_t u = __float_as_uint(v);
+    const auto p = S == 16 ? __builtin_amdgcn_permlane16_swap(u, u, false, false)
+                           : __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return __uint_as_float((__lane_id() & S) ? p[0] : p[1]);
+  }
+}
+
 // NaN-propagating max: once m is NaN it stays NaN.
 __device__ __forceinline__ float nan_max(float m, float v) { return (v != v || v > m) ? v : m; }
 
 __device__ __forceinline__ float block_nan_max(float m) {
   __shared__ float waves[kThreads / 64];
-#pragma unroll
-  for (int s = 1; s < 64; s <<= 1) m = nan_max(m, __shfl_xor(m, s, 64));
+  // Each lane folds in its partner's value, lane xor 1, 2, ..., 32: the
+  // butterfly every lane of the wave runs alike.
+  m = nan_max(m, lane_xor<1>(m));
+  m = nan_max(m, lane_xor<2>(m));
+  m = nan_max(m, lane_xor<4>(m));
+  m = nan_max(m, lane_xor<8>(m));
+  m = nan_max(m, lane_xor<16>(m));
+  m = nan_max(m, lane_xor<32>(m));
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   if (lane == 0) waves[wave] = m;
   __syncthreads();
