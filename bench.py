@@ -53,7 +53,8 @@ BASELINE shapes, each captured in a hipGraph and timed with events:
                     small prefill batches: one long row; one long row among
                     short ones
   mixed_tick        config 4: 4 x 256-token prefill + 96 decode rows on one
-                    192-slot fp16 pool; eager and graph-replayed per bucket
+                    192-slot fp16 pool; eager and graph-replayed per bucket, the
+                    decode beside the prefill (MixedTick) and in sequence
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
                        [--no-paths]
@@ -665,10 +666,17 @@ def measure_paths(torch, kern):
     py = torch.empty(4, 256, H, D, device=dev)
     plen = torch.full((4,), 256, dtype=torch.int32, device=dev)
     tick = {}
+    from braid_amd.tick import MixedTick
+    mixed = MixedTick(kern)
     for bucket in (16, 32, 64, 96, 128):
         live = min(bucket, 96)
-        # captured with distinct slots; pad rows then point at scratch slot 191
-        sl = torch.arange(bucket, dtype=torch.int32, device=dev)
+        # Captured (and run eagerly) with distinct slots apart from the prefill
+        # rows' 96..99: the live rows 0..live-1, then free slots 100..; the
+        # graphs are then replayed with the pad rows on one scratch slot, 191.
+        eager_sl = torch.cat([torch.arange(live, dtype=torch.int32, device=dev),
+                              torch.arange(100, 100 + bucket - live, dtype=torch.int32,
+                                           device=dev)])
+        sl = eager_sl.clone()
         padded = torch.cat([torch.arange(live, dtype=torch.int32, device=dev),
                             torch.full((bucket - live,), 191, dtype=torch.int32, device=dev)])
         dq = torch.randn(bucket, G, D, generator=g, device=dev)
@@ -678,26 +686,37 @@ def measure_paths(torch, kern):
         db = torch.randn(bucket, H, generator=g, device=dev).to(torch.bfloat16)
         dy = torch.empty(bucket, H, D, device=dev)
 
-        def tick_fn():
+        def tick_seq():
             kern.gdn_prefill_raw(pool, pre_slots, pq, pk, pv, pa, pb, A, dtb, py, plen)
             kern.gdn_decode_raw(pool, sl, dq, dk, dv, da, db, A, dtb, dy)
 
+        # The tick as the library runs it: the decode on a side stream beside
+        # the prefill (braid_amd/tick.py); the sequential tick beside it.
+        pre_args = dict(slots=pre_slots, q=pq, k=pk, v=pv, a_raw=pa, b_raw=pb, A=A,
+                        dt_bias=dtb, y=py, seq_lens=plen)
+        dec_args = dict(slots=sl, q=dq, k=dk, v=dv, a_raw=da, b_raw=db, A=A, dt_bias=dtb,
+                        y=dy)
+
+        def tick_fn():
+            mixed(pool, pre_args, dec_args)
+
         entry = {"graph_us": round(graph_time(torch, tick_fn, reps=11,
                                               before_replay=lambda: sl.copy_(padded)) * 1e6, 1)}
-        # eager: the kernels' eager validation wants distinct slots, so the
-        # pad rows of bucket 128 take distinct free slots (100..131; the
-        # prefill rows own 96..99) instead of one scratch slot
-        eager_sl = torch.cat([torch.arange(live, dtype=torch.int32, device=dev),
-                              torch.arange(100, 100 + bucket - live, dtype=torch.int32,
-                                           device=dev)])
         sl.copy_(eager_sl)
-        tick_fn()
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(5):
-            tick_fn()
-        torch.cuda.synchronize()
-        entry["eager_us"] = round((time.perf_counter() - t0) / 5 * 1e6, 1)
+        entry["graph_sequential_us"] = round(graph_time(
+            torch, tick_seq, reps=11, before_replay=lambda: sl.copy_(padded)) * 1e6, 1)
+        # eager: the kernels' eager validation wants distinct slots, so the
+        # pad rows of bucket 128 take distinct free slots (100..131) instead
+        # of one scratch slot
+        sl.copy_(eager_sl)
+        for label, fn in (("eager_us", tick_fn), ("eager_sequential_us", tick_seq)):
+            fn()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(5):
+                fn()
+            torch.cuda.synchronize()
+            entry[label] = round((time.perf_counter() - t0) / 5 * 1e6, 1)
         if bucket > live:
             entry["eager_pad"] = f"{bucket - live} pad rows on distinct free slots"
         tick[str(bucket)] = entry

@@ -16,6 +16,8 @@ import numpy as np
 import pytest
 import torch
 
+from braid_amd.tick import MixedTick
+
 import oracle
 from gpu_helpers import (ATOL, DEV, RTOL, act_np, assert_parity, gen, to_np_pool, torch_gates,
                          ulp16)
@@ -225,29 +227,47 @@ def test_config4_mixed_tick_eager_equals_graph_per_bucket(kern):
         y_pre = torch.empty(n_pre, T, H, D, device=DEV)
         y_dec = torch.empty(bucket, H, D, device=DEV)
 
-        def tick():
+        def tick_seq():
             kern.gdn_prefill_raw(pg, pre_slots, pre["q"], pre["k"], pre["v"], pre["a"],
                                  pre["b"], A, dtb, y_pre, seq)
             kern.gdn_decode_raw(pg, sl, bi["q"], bi["k"], bi["v"], bi["a"], bi["b"], A, dtb,
                                 y_dec)
 
-        graph = torch.cuda.CUDAGraph()
-        side = torch.cuda.Stream()
-        side.wait_stream(torch.cuda.current_stream())
-        if pad == 0:
-            with torch.cuda.stream(side):
-                tick()  # eager warm-up (validation on: slots distinct)
-            torch.cuda.current_stream().wait_stream(side)
-        with torch.cuda.graph(graph):
-            tick()
-        for _ in range(2):
-            pg.copy_(pool0)
-            graph.replay()
-            torch.cuda.synchronize()
-            assert torch.equal(y_pre, ye_pre), f"bucket {bucket}: prefill outputs"
-            assert torch.equal(y_dec[:live], ye_dec[:live]), f"bucket {bucket}: decode outputs"
-            assert torch.equal(pg[pre_slots.long()], pe[pre_slots.long()])
-            assert torch.equal(pg[dec_slots[:live].long()], pe[dec_slots[:live].long()])
+        # the same tick with the decode beside the prefill (MixedTick)
+        side_by_side = MixedTick(kern)
+        pre_args = dict(slots=pre_slots, q=pre["q"], k=pre["k"], v=pre["v"], a_raw=pre["a"],
+                        b_raw=pre["b"], A=A, dt_bias=dtb, y=y_pre, seq_lens=seq)
+        dec_args = dict(slots=sl, q=bi["q"], k=bi["k"], v=bi["v"], a_raw=bi["a"],
+                        b_raw=bi["b"], A=A, dt_bias=dtb, y=y_dec)
+
+        def tick_mixed():
+            side_by_side(pg, pre_args, dec_args)
+
+        def check(label):
+            assert torch.equal(y_pre, ye_pre), f"bucket {bucket} {label}: prefill outputs"
+            assert torch.equal(y_dec[:live], ye_dec[:live]), \
+                f"bucket {bucket} {label}: decode outputs"
+            assert torch.equal(pg[pre_slots.long()], pe[pre_slots.long()]), label
+            assert torch.equal(pg[dec_slots[:live].long()], pe[dec_slots[:live].long()]), label
             others = [s for s in range(S) if s >= live and s not in
                       (n_dec, n_dec + 1, n_dec + 2, n_dec + 3, scratch)]
-            assert torch.equal(pg[others], pool0[others])
+            assert torch.equal(pg[others], pool0[others]), label
+
+        for label, tick in (("sequential", tick_seq), ("side by side", tick_mixed)):
+            graph = torch.cuda.CUDAGraph()
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            if pad == 0:
+                pg.copy_(pool0)
+                with torch.cuda.stream(side):
+                    tick()  # eager (validation on: slots distinct)
+                torch.cuda.current_stream().wait_stream(side)
+                torch.cuda.synchronize()
+                check(label + ", eager")
+            with torch.cuda.graph(graph):
+                tick()
+            for _ in range(2):
+                pg.copy_(pool0)
+                graph.replay()
+                torch.cuda.synchronize()
+                check(label + ", graph")
