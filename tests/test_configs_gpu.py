@@ -234,7 +234,7 @@ def test_config4_mixed_tick_eager_equals_graph_per_bucket(kern):
                                 y_dec)
 
         # the same tick with the decode beside the prefill (MixedTick)
-        side_by_side = MixedTick(kern)
+        side_by_side = MixedTick(kern, check_slots=True)
         pre_args = dict(slots=pre_slots, q=pre["q"], k=pre["k"], v=pre["v"], a_raw=pre["a"],
                         b_raw=pre["b"], A=A, dt_bias=dtb, y=y_pre, seq_lens=seq)
         dec_args = dict(slots=sl, q=bi["q"], k=bi["k"], v=bi["v"], a_raw=bi["a"],
