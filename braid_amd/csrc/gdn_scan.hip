@@ -98,6 +98,9 @@ gdn_decode_kernel(typename Storage<Tag>::T* __restrict__ pool, const int* __rest
   normalize_qk_lds(L, q2, k2, qk_lds[L.wave], qk);
 
   float yy[CPL];
+  // Row-group sums through the permlane swaps, not the LDS crossbar: this
+  // kernel has the registers, and a B = 128 step gains 0.66 us (48.48 ->
+  // 47.82) from the shorter per-tile chain.
   gdn_token<Tag, CPL, true>(L, S, qk, vv, lds, yy);
 
 #pragma unroll
