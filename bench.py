@@ -431,8 +431,9 @@ def measure_paths(torch, kern):
     def prefill_case(lens):
         """Kernel time of the plan an eager call runs (chosen on the host from
         seq_lens, braid_prefill_plan), captured with that plan forced; beside
-        it the host's planning time and the time of a captured call, which
-        plans in the kernel."""
+        it the host's planning time, the time of a captured call, which plans
+        in the kernel, and of a captured call given the host lengths to plan
+        from (plan_lens)."""
         Bp, T = len(lens), max(lens)
         pool = (torch.randn(Bp + 4, H, D, D, generator=g, device=dev) * 0.02).half()
         slots = torch.arange(2, Bp + 2, dtype=torch.int32, device=dev)
@@ -464,6 +465,10 @@ def measure_paths(torch, kern):
         with kern.launch_override(**knobs):
             t = graph_time(torch, call, reps=11)
         t_dev = graph_time(torch, call, reps=11)
+        # a captured call handed the host lengths to plan from (plan_lens)
+        t_hint = graph_time(torch, lambda: kern.gdn_prefill_raw(pool, slots, q, k, v, a, b, A,
+                                                                dtb, y, sl, plan_lens=lens),
+                            reps=11)
         tok = sum(lens)
         tf = tok * H * FLOP_PER_TOKEN_HEAD / t / 1e12
         return {"rows": Bp, "max_T": T, "tokens": tok, "ms": round(t * 1e3, 3),
@@ -471,7 +476,8 @@ def measure_paths(torch, kern):
                 "fp32_frac": round(tf / FP32_PEAK_TFLOPS, 4),
                 "plan": {"eighth_rows": n8, "quarter_rows": n4, "split_rows": n2},
                 "host_plan_us": round(min(plan_times) * 1e6, 1),
-                "captured_kernel_plan_ms": round(t_dev * 1e3, 3)}
+                "captured_kernel_plan_ms": round(t_dev * 1e3, 3),
+                "captured_plan_lens_ms": round(t_hint * 1e3, 3)}
 
     # the config-1 step on bf16 and fp32 pools (one 160-slot pool each; an fp32
     # pool is 320 MiB, past the 256 MB MALL; the bf16 pool's figure is hot)

@@ -1271,7 +1271,8 @@ int host_prefill_plan(const std::vector<int32_t>& seq_lens, int T, int H, int cu
 template <class Gates>
 int launch_prefill(void* pool, int pool_dtype, const int32_t* slot_idx, int B, int T, int H,
                    int G, const float* q, const float* k, const float* v, Gates gates,
-                   float* y, const std::vector<int32_t>* host_lens, hipStream_t stream) {
+                   float* y, const std::vector<int32_t>* host_lens, hipStream_t stream,
+                   int plan_hint = -1) {
   const int cus = device_cus();
   int layout = prefill_layout(B * H, B, gates.ragged(), cus);
   // With the live lengths on the host, every ragged batch the planned kernel
@@ -1285,6 +1286,16 @@ int launch_prefill(void* pool, int pool_dtype, const int32_t* slot_idx, int B, i
       B * H <= 4 * cus) {
     host_plan = host_prefill_plan(*host_lens, T, H, cus);
     const int n8 = host_plan >> 20, n4 = (host_plan >> 10) & 1023, n2 = host_plan & 1023;
+    layout = n8 == B ? 8 : (n4 == B ? 4 : (n2 == B ? 1 : 0));
+  } else if (plan_hint >= 0 && gates.ragged() && layout != 8 &&
+             launch_knob(BRAID_KNOB_PREFILL_LAYOUT) < 0 &&
+             launch_knob(BRAID_KNOB_PREFILL_PLAN) < 0 && B <= kMaxPlanRows && cus > 0 &&
+             B * H <= 4 * cus) {
+    // The caller's plan (braid_gdn_prefill_raw_plan), taken as the host's.
+    const int n8 = std::min(plan_hint >> 20, B);
+    const int n4 = std::min((plan_hint >> 10) & 1023, B - n8);
+    const int n2 = std::min(plan_hint & 1023, B - n8 - n4);
+    host_plan = (n8 << 20) | (n4 << 10) | n2;
     layout = n8 == B ? 8 : (n4 == B ? 4 : (n2 == B ? 1 : 0));
   }
   if (layout == 8)
@@ -1397,12 +1408,14 @@ extern "C" int braid_gdn_prefill(void* pool, int pool_dtype, int64_t n_slots, in
                         PrecomputedGates{alpha, beta}, y, nullptr, stream);
 }
 
-extern "C" int braid_gdn_prefill_raw(void* pool, int pool_dtype, int64_t n_slots, int H, int G,
-                                     int SS, int HD, const int32_t* slot_idx, int B, int T,
-                                     const float* q, const float* k, const float* v,
-                                     const void* a_raw, const void* b_raw, int act_dtype,
-                                     const float* A, const float* dt_bias, float* y,
-                                     const int32_t* seq_lens, void* stream_) {
+namespace braid {
+namespace {
+
+int prefill_raw(void* pool, int pool_dtype, int64_t n_slots, int H, int G, int SS, int HD,
+                const int32_t* slot_idx, int B, int T, const float* q, const float* k,
+                const float* v, const void* a_raw, const void* b_raw, int act_dtype,
+                const float* A, const float* dt_bias, float* y, const int32_t* seq_lens,
+                int plan_hint, void* stream_) {
   hipStream_t stream = static_cast<hipStream_t>(stream_);
   BRAID_TRY(check_common(pool, pool_dtype, n_slots, H, G, SS, HD, slot_idx, B));
   if (T < 0) return fail(BRAID_EINVAL, "T must be non-negative");
@@ -1433,12 +1446,37 @@ extern "C" int braid_gdn_prefill_raw(void* pool, int pool_dtype, int64_t n_slots
     RawGates<F32> gates{static_cast<const float*>(a_raw), static_cast<const float*>(b_raw), A,
                         dt_bias, seq_lens};
     return launch_prefill(pool, pool_dtype, slot_idx, B, T, H, G, q, k, v, gates, y, lens_p,
-                          stream);
+                          stream, plan_hint);
   }
   RawGates<BF16> gates{static_cast<const uint16_t*>(a_raw), static_cast<const uint16_t*>(b_raw),
                        A, dt_bias, seq_lens};
   return launch_prefill(pool, pool_dtype, slot_idx, B, T, H, G, q, k, v, gates, y, lens_p,
-                        stream);
+                        stream, plan_hint);
+}
+
+}  // namespace
+}  // namespace braid
+
+extern "C" int braid_gdn_prefill_raw(void* pool, int pool_dtype, int64_t n_slots, int H, int G,
+                                     int SS, int HD, const int32_t* slot_idx, int B, int T,
+                                     const float* q, const float* k, const float* v,
+                                     const void* a_raw, const void* b_raw, int act_dtype,
+                                     const float* A, const float* dt_bias, float* y,
+                                     const int32_t* seq_lens, void* stream_) {
+  return prefill_raw(pool, pool_dtype, n_slots, H, G, SS, HD, slot_idx, B, T, q, k, v, a_raw,
+                     b_raw, act_dtype, A, dt_bias, y, seq_lens, -1, stream_);
+}
+
+extern "C" int braid_gdn_prefill_raw_plan(void* pool, int pool_dtype, int64_t n_slots, int H,
+                                          int G, int SS, int HD, const int32_t* slot_idx, int B,
+                                          int T, const float* q, const float* k, const float* v,
+                                          const void* a_raw, const void* b_raw, int act_dtype,
+                                          const float* A, const float* dt_bias, float* y,
+                                          const int32_t* seq_lens, int plan, void* stream_) {
+  if (plan >= 0 && seq_lens == nullptr)
+    return fail(BRAID_EINVAL, "a prefill plan needs seq_lens (it plans ragged batches)");
+  return prefill_raw(pool, pool_dtype, n_slots, H, G, SS, HD, slot_idx, B, T, q, k, v, a_raw,
+                     b_raw, act_dtype, A, dt_bias, y, seq_lens, plan, stream_);
 }
 
 namespace braid {

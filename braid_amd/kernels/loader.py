@@ -32,7 +32,7 @@ import contextlib
 import ctypes
 from functools import lru_cache
 from pathlib import Path
-from typing import Optional
+from typing import Optional, Sequence
 
 import torch
 
@@ -64,6 +64,9 @@ SIGNATURES = {
     "braid_gdn_prefill_raw": ([_vp, _i32, _i64, _i32, _i32, _i32, _i32, _vp, _i32, _i32,
                                _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp,
                                _vp], _i32),
+    "braid_gdn_prefill_raw_plan": ([_vp, _i32, _i64, _i32, _i32, _i32, _i32, _vp, _i32, _i32,
+                                    _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp,
+                                    _i32, _vp], _i32),
     "braid_gdn_conv_decode_raw": ([_vp, _i32, _i64, _i32, _i32, _i32, _i32, _vp, _i32, _vp,
                                    _i32, _vp, _i32, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp,
                                    _vp], _i32),
@@ -288,9 +291,17 @@ class GDNKernels:
                    _ptr(beta), _ptr(y))
 
     def gdn_prefill_raw(self, pool, slot_idx, q, k, v, a_raw, b_raw, A, dt_bias, y,
-                        seq_lens: Optional[torch.Tensor] = None) -> None:
+                        seq_lens: Optional[torch.Tensor] = None,
+                        plan_lens: Optional[Sequence[int]] = None) -> None:
         """Chunk scan with in-kernel gates and ragged seq_lens
-        (gdn_decode.cu:611-699). seq_lens=None means every column is live."""
+        (gdn_decode.cu:611-699). seq_lens=None means every column is live.
+
+        ``plan_lens``: the row lengths, on the host, to plan a ragged launch
+        from when the call cannot read ``seq_lens`` itself, that is under graph
+        capture (an eager call plans from ``seq_lens`` and ignores it). A
+        graph captured with them keeps that plan for every replay; the results
+        are the same bits for whatever lengths a replay holds, only the time
+        depends on the plan. Not in the reference, whose prefill is eager."""
         pdt = _check_pool(pool, slot_idx)
         _check_dense_f32((q, k, v, y), "q/k/v/y must be contiguous cuda fp32")
         adt = _check_raw(a_raw, b_raw, A, dt_bias)
@@ -303,9 +314,27 @@ class GDNKernels:
             _check(seq_lens.is_cuda and seq_lens.dtype == torch.int32
                    and seq_lens.is_contiguous(), "seq_lens must be contiguous cuda int32")
             _check(seq_lens.numel() == B, "seq_lens must have one entry per batch row")
-        self._call("braid_gdn_prefill_raw", pool.device, _ptr(pool), pdt, pool.size(0), H, G,
-                   SS, HD, _ptr(slot_idx), B, T, _ptr(q), _ptr(k), _ptr(v), _ptr(a_raw),
-                   _ptr(b_raw), adt, _ptr(A), _ptr(dt_bias), _ptr(y), _ptr(seq_lens))
+        if plan_lens is None:
+            self._call("braid_gdn_prefill_raw", pool.device, _ptr(pool), pdt, pool.size(0), H,
+                       G, SS, HD, _ptr(slot_idx), B, T, _ptr(q), _ptr(k), _ptr(v), _ptr(a_raw),
+                       _ptr(b_raw), adt, _ptr(A), _ptr(dt_bias), _ptr(y), _ptr(seq_lens))
+            return
+        _check(seq_lens is not None, "plan_lens plans a ragged batch: seq_lens is required")
+        _check(len(plan_lens) == B, "plan_lens must have one entry per batch row")
+        plan = self.prefill_plan(plan_lens, T, H, pool.device)
+        self._call("braid_gdn_prefill_raw_plan", pool.device, _ptr(pool), pdt, pool.size(0), H,
+                   G, SS, HD, _ptr(slot_idx), B, T, _ptr(q), _ptr(k), _ptr(v), _ptr(a_raw),
+                   _ptr(b_raw), adt, _ptr(A), _ptr(dt_bias), _ptr(y), _ptr(seq_lens), plan)
+
+    def prefill_plan(self, lens: Sequence[int], T: int, H: int, device=None) -> int:
+        """The plan (n8 * 2^20 + n4 * 2^10 + n2) an eager ragged prefill of
+        these host lengths runs on ``device`` (braid_prefill_plan)."""
+        cus = torch.cuda.get_device_properties(device).multi_processor_count
+        arr = (ctypes.c_int32 * len(lens))(*[int(x) for x in lens])
+        plan = self._lib.braid_prefill_plan(ctypes.cast(arr, ctypes.c_void_p), len(lens), T, H,
+                                            cus)
+        _check(plan >= 0, self._lib.braid_last_error().decode())
+        return plan
 
     @staticmethod
     def _check_prefill_shapes(pool, slot_idx, q, k, v, y):

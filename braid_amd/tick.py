@@ -32,10 +32,12 @@ from braid_amd.kernels.loader import load_gdn
 class MixedTick:
     """``tick(pool, prefill, decode)`` with ``prefill`` the arguments of
     ``gdn_prefill_raw`` after the pool (slots, q, k, v, a_raw, b_raw, A,
-    dt_bias, y, seq_lens) and ``decode`` those of ``gdn_decode_raw`` (slots,
-    q, k, v, a_raw, b_raw, A, dt_bias, y), as dicts with those names. The
-    prefill runs on the caller's current stream, the decode on this object's
-    side stream; the caller's stream waits for both before it goes on."""
+    dt_bias, y, seq_lens, and optionally plan_lens: the host lengths a
+    captured tick plans its ragged prefill from) and ``decode`` those of
+    ``gdn_decode_raw`` (slots, q, k, v, a_raw, b_raw, A, dt_bias, y), as
+    dicts with those names. The prefill runs on the caller's current stream,
+    the decode on this object's side stream; the caller's stream waits for
+    both before it goes on."""
 
     PREFILL = ("slots", "q", "k", "v", "a_raw", "b_raw", "A", "dt_bias", "y", "seq_lens")
     DECODE = ("slots", "q", "k", "v", "a_raw", "b_raw", "A", "dt_bias", "y")
@@ -61,6 +63,7 @@ class MixedTick:
 
     def __call__(self, pool: torch.Tensor, prefill: dict, decode: dict) -> None:
         pre = [prefill[k] for k in self.PREFILL]
+        plan = {"plan_lens": prefill["plan_lens"]} if "plan_lens" in prefill else {}
         dec = [decode[k] for k in self.DECODE]
         if not torch.cuda.is_current_stream_capturing():
             # Eager: in sequence, on the caller's stream. Each eager launch
@@ -72,12 +75,12 @@ class MixedTick:
             # about 28 us at config 4).
             if self.check_slots:
                 self._check_disjoint(prefill["slots"], decode["slots"])
-            self.kern.gdn_prefill_raw(pool, *pre)
+            self.kern.gdn_prefill_raw(pool, *pre, **plan)
             self.kern.gdn_decode_raw(pool, *dec)
             return
         main = torch.cuda.current_stream(pool.device)
         self.side.wait_stream(main)
-        self.kern.gdn_prefill_raw(pool, *pre)
+        self.kern.gdn_prefill_raw(pool, *pre, **plan)
         with torch.cuda.stream(self.side):
             self.kern.gdn_decode_raw(pool, *dec)
         main.wait_stream(self.side)

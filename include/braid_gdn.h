@@ -183,6 +183,24 @@ int braid_gdn_prefill_raw(void* pool, int pool_dtype, int64_t n_slots, int H,
                           float* y, const int32_t* seq_lens, void* stream);
 
 /*
+ * braid_gdn_prefill_raw with the caller's launch plan for a ragged batch
+ * (plan: what braid_prefill_plan returns for the lengths the caller expects,
+ * or < 0 for none). An eager call reads seq_lens on the host and plans from
+ * them, so it ignores the plan; a call under graph capture cannot, and
+ * without a plan it runs the kernel's own cruder estimate. Any plan computes
+ * the same bits for any lengths (the kernel ranks the rows by their actual
+ * lengths); the plan only shapes the launch. A plan needs seq_lens
+ * (BRAID_EINVAL without). No counterpart in the reference, whose prefill is
+ * not captured.
+ */
+int braid_gdn_prefill_raw_plan(void* pool, int pool_dtype, int64_t n_slots, int H,
+                               int G, int SS, int HD, const int32_t* slot_idx,
+                               int B, int T, const float* q, const float* k,
+                               const float* v, const void* a_raw, const void* b_raw,
+                               int act_dtype, const float* A, const float* dt_bias,
+                               float* y, const int32_t* seq_lens, int plan, void* stream);
+
+/*
  * Batched slotted causal depthwise conv1d, one decode step, SiLU fused.
  * Replaces conv1d_decode (braid/kernels/csrc/conv1d_decode.cu:91-149).
  *

@@ -425,3 +425,47 @@ def test_host_planned_eager_prefill_equals_the_captured_one(kern):
         assert torch.equal(yt[0], ye[r, t]), t
     torch.cuda.synchronize()
     assert torch.equal(ps[slots[r]].view(torch.int16), pe[slots[r]].view(torch.int16))
+
+
+def test_a_captured_prefill_with_a_host_plan_equals_the_eager_one(kern):
+    """Under capture the caller can hand the library the plan it would choose
+    from host lengths (plan_lens). The graph keeps that plan; replayed over the
+    lengths it was planned for and over other lengths, it leaves the eager
+    prefill's bits, since every plan computes the same bits."""
+    lens_l = [454, 610, 334, 542, 393, 861, 814, 65]
+    B, T, H, G = len(lens_l), max(lens_l), 32, 16
+    inp = prefill_inputs(B, T, H=H, G=G, seed=81)
+    a, b, A, dtb = raw_gates((B, T, H), H, torch.bfloat16, seed=82)
+    lens = torch.tensor(lens_l, dtype=torch.int32, device=DEV)
+    slots = torch.arange(1, B + 1, dtype=torch.int32, device=DEV)
+    base = pool(B + 2, H=H, dtype=torch.float16)
+    assert kern.prefill_plan(lens_l, T, H) != 0  # a mixed plan, not all-whole
+    pg, yg = base.clone(), torch.empty(B, T, H, 128, device=DEV)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        kern.gdn_prefill_raw(pg, slots, inp["q"], inp["k"], inp["v"], a, b, A, dtb, yg, lens,
+                             plan_lens=lens_l)
+    torch.cuda.current_stream().wait_stream(s)
+    for replay_lens in (lens_l, [T, 1, 0, 300, 861, 2, 700, 64]):
+        lens.copy_(torch.tensor(replay_lens, dtype=torch.int32))
+        pe, ye = base.clone(), torch.empty(B, T, H, 128, device=DEV)
+        kern.gdn_prefill_raw(pe, slots, inp["q"], inp["k"], inp["v"], a, b, A, dtb, ye, lens)
+        pg.copy_(base)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(pe.view(torch.int16), pg.view(torch.int16)), replay_lens
+        assert torch.equal(ye, yg), replay_lens
+
+
+def test_a_plan_needs_seq_lens(kern):
+    B, T, H, G = 2, 8, 32, 16
+    inp = prefill_inputs(B, T, H=H, G=G, seed=83)
+    a, b, A, dtb = raw_gates((B, T, H), H, torch.bfloat16, seed=84)
+    p = pool(4, H=H, dtype=torch.float16)
+    y = torch.empty(B, T, H, 128, device=DEV)
+    slots = torch.arange(B, dtype=torch.int32, device=DEV)
+    with pytest.raises(RuntimeError, match="seq_lens is required"):
+        kern.gdn_prefill_raw(p, slots, inp["q"], inp["k"], inp["v"], a, b, A, dtb, y,
+                             plan_lens=[T, T])
