@@ -100,11 +100,13 @@ class GDNMixerLayer:
 
     def prefill(self, qkv_proj: torch.Tensor, z: torch.Tensor, a_raw: torch.Tensor,
                 b_raw: torch.Tensor, cache: RecurrentCache, slots_i32: torch.Tensor,
-                seq_lens: Optional[torch.Tensor] = None):
+                seq_lens: Optional[torch.Tensor] = None, plan_lens: Optional[list] = None):
         """T tokens per row, right-padded when ``seq_lens`` is given (row b owns
         columns 0..seq_lens[b]-1): conv prefill, raw-gates chunk scan, readout
         (gdn.py:171-226 and :273-291). Pad columns leave the conv window and the
-        state exactly as the row's last live token left them."""
+        state exactly as the row's last live token left them. ``plan_lens``: the
+        same lengths on the host, for a captured call to plan its ragged scan
+        from (``gdn_prefill_raw``); the bits do not depend on it."""
         g = self.g
         if cache is None or slots_i32 is None:
             raise ValueError("a pooled cache needs a slot assignment")
@@ -118,7 +120,8 @@ class GDNMixerLayer:
                         dtype=torch.float32)
         self._mod.gdn_prefill_raw(cache.state, slots_i32, q.contiguous(), k.contiguous(),
                                   v.contiguous(), a_raw.contiguous(), b_raw.contiguous(),
-                                  self.A, self.dt_bias, y, lens)
+                                  self.A, self.dt_bias, y, lens,
+                                  plan_lens=plan_lens if lens is not None else None)
         return self._readout(z, y)
 
 
