@@ -78,6 +78,9 @@ class MixedTick:
             self.kern.gdn_prefill_raw(pool, *pre, **plan)
             self.kern.gdn_decode_raw(pool, *dec)
             return
+        if self.side.device != pool.device:
+            raise RuntimeError(f"this MixedTick's side stream is on {self.side.device}, "
+                               f"the pool on {pool.device}")
         main = torch.cuda.current_stream(pool.device)
         self.side.wait_stream(main)
         self.kern.gdn_prefill_raw(pool, *pre, **plan)
