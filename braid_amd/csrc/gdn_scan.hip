@@ -959,8 +959,8 @@ int device_cus() {
 // Column parts of a decode launch (gdn_decode_kernel): 2 when a launch has
 // at most as many tiles as the GPU has CUs, else 1. Measured per step on
 // MI355X (fp16 pool, H = 32, cold slots, graph-replayed), parts 1 / 2 / 4:
-// B=1 4.23 / 3.51 / 3.65 us, B=4 4.61 / 3.89 / 5.21, B=8 5.31 / 4.97 / 7.87,
-// B=16 7.15 / 8.28 / 12.54. Four parts never win: two columns per lane make
+// B=1 3.95 / 3.31 / 3.55 us, B=4 4.56 / 3.88 / 4.99, B=8 5.33 / 4.84 / 7.74,
+// B=16 7.20 / 8.65 / 12.29. Four parts never win: two columns per lane make
 // every state access 4 bytes. The DECODE_PARTS launch knob (1, 2 or 4)
 // overrides the choice.
 int decode_parts(long n_tiles, int cus) {
