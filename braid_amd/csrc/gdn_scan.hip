@@ -1039,13 +1039,22 @@ int launch_decode(void* pool, int pool_dtype, const int32_t* slot_idx, int B, in
 // layout 4 would put two workgroups on every CU, 0.183 in layout 1 against
 // 0.190 ms; one 512-token row in layout 8 0.126 ms against 0.164 in layout
 // 4, 1024 tokens 0.245 against 0.320 (half the VALU per token again, and the
-// column sums inside 16-lane rows). The PREFILL_LAYOUT launch knob (1, 2, 4,
-// 8, or 0 for planned when seq_lens is given) overrides the choice.
-int prefill_layout(int n_tiles, int B, bool ragged, int cus) {
+// column sums inside 16-lane rows). With up to two eighth-layout workgroups
+// per CU the eighth layout still wins once the chunk is long enough for its
+// per-token cost to outweigh the shared CU (two rows of H = 32, quarter
+// against eighth: T = 64 0.0265 against 0.030 ms, T = 256 0.0879 against
+// 0.0844, T = 1024 0.325 against 0.305; at three rows, three per CU, the
+// eighth loses, 0.130 against 0.119 in layout 1). The PREFILL_LAYOUT launch
+// knob (1, 2, 4, 8, or 0 for planned when seq_lens is given) overrides the
+// choice.
+constexpr int kEighthSharedMinT = 256;
+
+int prefill_layout(int n_tiles, int B, int T, bool ragged, int cus) {
   const int forced = launch_knob(BRAID_KNOB_PREFILL_LAYOUT);
   if (forced == 1 || forced == 2 || forced == 4 || forced == 8) return forced;
   if (forced == 0 && ragged && B <= kMaxPlanRows) return 0;
   if (cus > 0 && 8 * n_tiles <= cus) return 8;
+  if (cus > 0 && 8 * n_tiles <= 2 * cus && T >= kEighthSharedMinT) return 8;
   if (cus > 0 && 4 * n_tiles <= cus) return 4;
   if (cus > 0 && 2 * n_tiles <= cus) return 1;
   return ragged && B <= kMaxPlanRows && cus > 0 && n_tiles <= 4 * cus ? 0 : 2;
@@ -1303,7 +1312,7 @@ int launch_prefill(void* pool, int pool_dtype, const int32_t* slot_idx, int B, i
                    float* y, const std::vector<int32_t>* host_lens, hipStream_t stream,
                    int plan_hint = -1) {
   const int cus = device_cus();
-  int layout = prefill_layout(B * H, B, gates.ragged(), cus);
+  int layout = prefill_layout(B * H, B, T, gates.ragged(), cus);
   // With the live lengths on the host, every ragged batch the planned kernel
   // takes is planned there. A plan that puts every row in one tier runs that
   // layout's own kernel instead (its split layout runs token pairs, which
