@@ -1,6 +1,7 @@
 // Error reporting and slot validation for the C ABI (host code only).
 #include "capi_common.h"
 
+#include <algorithm>
 #include <atomic>
 #include <cstdlib>
 #include <vector>
@@ -53,19 +54,59 @@ bool stream_capturing(hipStream_t stream, int* status) {
   return cs != hipStreamCaptureStatusNone;
 }
 
+namespace {
+// Pinned host memory for the eager checks' small device-to-host copies, per
+// thread, grown on demand: a copy into pageable memory is staged through a
+// driver buffer and costs more. Never freed (no destructor), so nothing runs
+// against the HIP runtime while the process exits; a thread that made an
+// eager call keeps its buffer (1 KiB for up to 128 rows with lengths).
+struct Staging {
+  int32_t* p = nullptr;
+  size_t cap = 0;
+};
+thread_local Staging g_staging;
+
+int32_t* staging(size_t count, int* status) {
+  if (count > g_staging.cap) {
+    if (g_staging.p != nullptr) (void)hipHostFree(g_staging.p);
+    g_staging.p = nullptr;
+    g_staging.cap = 0;
+    size_t cap = 256;
+    while (cap < count) cap *= 2;
+    void* p = nullptr;
+    *status = hip_status(hipHostMalloc(&p, cap * sizeof(int32_t), hipHostMallocDefault),
+                         "allocating pinned host memory for the slot check");
+    if (*status != BRAID_OK) return nullptr;
+    g_staging.p = static_cast<int32_t*>(p);
+    g_staging.cap = cap;
+  }
+  *status = BRAID_OK;
+  return g_staging.p;
+}
+}  // namespace
+
 int validate_slots(const int32_t* slot_idx, int B, int64_t n_slots, bool distinct,
-                   hipStream_t stream) {
+                   hipStream_t stream, const int32_t* lens_dev, int32_t* lens_host) {
   int st = BRAID_OK;
   if (stream_capturing(stream, &st)) return BRAID_OK;
   if (st != BRAID_OK) return st;
   if (B == 0) return BRAID_OK;
-  std::vector<int32_t> host(B);
-  st = hip_status(hipMemcpyAsync(host.data(), slot_idx, sizeof(int32_t) * (size_t)B,
+  const bool with_lens = lens_dev != nullptr && lens_host != nullptr;
+  int32_t* host = staging((size_t)B * (with_lens ? 2 : 1), &st);
+  if (st != BRAID_OK) return st;
+  if (with_lens) {
+    st = hip_status(hipMemcpyAsync(host + B, lens_dev, sizeof(int32_t) * (size_t)B,
+                                   hipMemcpyDeviceToHost, stream),
+                    "copying seq_lens to the host");
+    if (st != BRAID_OK) return st;
+  }
+  st = hip_status(hipMemcpyAsync(host, slot_idx, sizeof(int32_t) * (size_t)B,
                                  hipMemcpyDeviceToHost, stream),
                   "copying slot_idx to the host");
   if (st != BRAID_OK) return st;
   st = hip_status(hipStreamSynchronize(stream), "synchronizing for slot validation");
   if (st != BRAID_OK) return st;
+  if (with_lens) std::copy(host + B, host + 2 * (size_t)B, lens_host);
   std::vector<char> seen(distinct ? (size_t)n_slots : 0, 0);
   for (int i = 0; i < B; ++i) {
     const int32_t s = host[i];

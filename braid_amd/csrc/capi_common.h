@@ -27,8 +27,11 @@ bool stream_capturing(hipStream_t stream, int* status);
 // entry lies in [0, n_slots); with `distinct`, also that no slot repeats.
 // Message fragments follow braid/kernels/csrc/gdn_decode.cu:289-296:
 // "... is out of range [0, n)" and "duplicate slot ... must be distinct".
+// With lens_dev and lens_host, the same round trip also copies
+// lens_dev[0..B) into lens_host (left untouched while capturing).
 int validate_slots(const int32_t* slot_idx, int B, int64_t n_slots, bool distinct,
-                   hipStream_t stream);
+                   hipStream_t stream, const int32_t* lens_dev = nullptr,
+                   int32_t* lens_host = nullptr);
 
 // Launch knobs, for measurement: overrides of the launch-shape choices,
 // -1 when unset. Initialised once from the environment when the library

@@ -1465,20 +1465,16 @@ int prefill_raw(void* pool, int pool_dtype, int64_t n_slots, int H, int G, int S
     BRAID_TRY(check_dense(v, "v"));
     BRAID_TRY(check_dense(y, "y"));
   }
-  // An eager call reads the live lengths on the host for the ragged plan: the
-  // copy is ordered before the slot map's and completes with its
-  // synchronisation.
+  // An eager call reads the live lengths on the host for the ragged plan, in
+  // the slot check's round trip (one synchronisation for both copies).
   std::vector<int32_t> host_lens;
   int cap_st = BRAID_OK;
   const bool capturing = stream_capturing(stream, &cap_st);
   if (cap_st != BRAID_OK) return cap_st;
-  if (seq_lens != nullptr && !capturing && T > 0) {
-    host_lens.resize(B);
-    BRAID_TRY(hip_status(hipMemcpyAsync(host_lens.data(), seq_lens, sizeof(int32_t) * (size_t)B,
-                                        hipMemcpyDeviceToHost, stream),
-                         "copying seq_lens to the host"));
-  }
-  BRAID_TRY(validate_slots(slot_idx, B, n_slots, true, stream));
+  if (seq_lens != nullptr && !capturing && T > 0) host_lens.resize(B);
+  BRAID_TRY(validate_slots(slot_idx, B, n_slots, true, stream,
+                           host_lens.empty() ? nullptr : seq_lens,
+                           host_lens.empty() ? nullptr : host_lens.data()));
   const std::vector<int32_t>* lens_p = host_lens.empty() ? nullptr : &host_lens;
   if (act_dtype == BRAID_F32) {
     RawGates<F32> gates{static_cast<const float*>(a_raw), static_cast<const float*>(b_raw), A,
