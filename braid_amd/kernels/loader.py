@@ -118,14 +118,20 @@ def _row_stride_3d(t: torch.Tensor, name: str, require_cuda: bool = True) -> int
     """Batch stride of a [B, X, Y] fp32 operand whose last two dims are dense
     (gdn_decode.cu:303-311): only the batch stride may differ, and rows may
     not overlap."""
-    _check((t.is_cuda or not require_cuda) and t.dtype == torch.float32,
-           f"{name} must be cuda fp32")
-    _check(t.dim() == 3, f"{name} must be 3-d")
-    _check(t.stride(2) == 1 and t.stride(1) == t.size(2),
-           f"{name} must be dense in its last two dims (only the batch stride may "
-           f"differ; got strides {tuple(t.stride())})")
-    _check(t.size(0) <= 1 or t.stride(0) >= t.size(1) * t.size(2), f"{name} rows overlap")
-    return max(t.stride(0), t.size(1) * t.size(2))
+    # The messages are built only on failure: formatting them on every call
+    # cost more than the checks.
+    if not ((t.is_cuda or not require_cuda) and t.dtype == torch.float32):
+        raise RuntimeError(f"{name} must be cuda fp32")
+    if t.dim() != 3:
+        raise RuntimeError(f"{name} must be 3-d")
+    s0, s1, s2 = t.stride()
+    n0, n1, n2 = t.shape
+    if not (s2 == 1 and s1 == n2):
+        raise RuntimeError(f"{name} must be dense in its last two dims (only the batch stride "
+                           f"may differ; got strides {(s0, s1, s2)})")
+    if not (n0 <= 1 or s0 >= n1 * n2):
+        raise RuntimeError(f"{name} rows overlap")
+    return max(s0, n1 * n2)
 
 
 def _check_pool(pool: torch.Tensor, slot_idx: torch.Tensor) -> int:
@@ -164,9 +170,15 @@ class GDNKernels:
     # -- plumbing -------------------------------------------------------------
 
     def _call(self, fn_name: str, device: torch.device, *args) -> None:
-        with torch.cuda.device(device):
-            stream = torch.cuda.current_stream(device).cuda_stream
-            rc = getattr(self._lib, fn_name)(*args, stream)
+        # The library launches on the current HIP device; switch to the
+        # operands' device only when it is another one (the switch costs
+        # about 3 us a call).
+        if device.index is None or device.index == torch.cuda.current_device():
+            rc = getattr(self._lib, fn_name)(*args, torch.cuda.current_stream().cuda_stream)
+        else:
+            with torch.cuda.device(device):
+                stream = torch.cuda.current_stream(device).cuda_stream
+                rc = getattr(self._lib, fn_name)(*args, stream)
         if rc != 0:
             raise RuntimeError(self._lib.braid_last_error().decode())
 
