@@ -39,8 +39,15 @@ namespace {
 // to spread each tile's arithmetic over more CUs (its latency is the
 // per-lane work, which shrinks with the columns). fp32 pools split a lane's
 // columns into two runs 64 apart only with one part.
-template <class Tag, class Gates, int P>
+//
+// kWavesPerSimd bounds the register budget: 4 (128 VGPRs) where up to four
+// workgroups share a CU; 2 for the large launches that stream_shape caps at
+// two workgroups per CU, where 256 VGPRs cost no residency and the compiler
+// schedules the prologue's loads more freely (169 VGPRs; B = 128: 47.92 ->
+// 47.63 us a step in one A/B run).
+template <class Tag, class Gates, int P, int kWavesPerSimd = 4>
 __global__ void __launch_bounds__(tile_threads(kDecodeCols))
+__attribute__((amdgpu_waves_per_eu(1, kWavesPerSimd)))
 gdn_decode_kernel(typename Storage<Tag>::T* __restrict__ pool, const int* __restrict__ slot_idx,
                   const float* __restrict__ q, const float* __restrict__ k,
                   const float* __restrict__ v, Gates gates, float* __restrict__ y, int H,
@@ -980,9 +987,21 @@ void launch_decode_as(void* pool, const int32_t* slot_idx, int B, int H, int G, 
                    sizeof(TileLds) + kWaves * sizeof(QKLds),
                    launch_knob(BRAID_KNOB_DECODE_XCD_REMAP),
                    launch_knob(BRAID_KNOB_DECODE_WGS_PER_CU));
+  // A launch capped at two resident workgroups per CU (its LDS request) takes
+  // the two-waves-per-SIMD register budget.
+  constexpr size_t kLdsPerCu = 160 * 1024;
+  const size_t lds_per_wg = shape.lds_pad + sizeof(TileLds) + kWaves * sizeof(QKLds);
+  if constexpr (P == 1 && !std::is_same<Tag, F32>::value) {
+    if (shape.lds_pad > 0 && kLdsPerCu / lds_per_wg <= 2) {
+      gdn_decode_kernel<Tag, Gates, P, 2><<<grid, block, shape.lds_pad, stream>>>(
+          static_cast<typename Storage<Tag>::T*>(pool), slot_idx, q, k, v, gates, y, H, H / G,
+          q_row, k_row, v_row, shape.xcd_per);
+      return;
+    }
+  }
   gdn_decode_kernel<Tag, Gates, P><<<grid, block, shape.lds_pad, stream>>>(
-      static_cast<typename Storage<Tag>::T*>(pool), slot_idx, q, k, v, gates, y, H, H / G, q_row,
-      k_row, v_row, shape.xcd_per);
+      static_cast<typename Storage<Tag>::T*>(pool), slot_idx, q, k, v, gates, y, H, H / G,
+      q_row, k_row, v_row, shape.xcd_per);
 }
 
 template <class Tag, class Gates>

@@ -77,7 +77,8 @@ def test_decode_state_uses_128_bit_nontemporal_accesses(asm):
 def test_decode_kernels_fit_four_waves_per_simd(asm):
     """The decode kernels are bound by the state stream, which needs four
     resident workgroups per CU (four waves per SIMD) to keep enough bytes in
-    flight; that holds only at <= 128 architectural VGPRs per lane. Every
+    flight; that holds only at <= 128 architectural VGPRs per lane (except
+    the instantiations for launches held to two workgroups per CU). Every
     instantiation (each pool dtype and gate policy, fused conv or not) is
     checked: the compiler's register count moves with small changes to the
     body's order."""
@@ -89,6 +90,10 @@ def test_decode_kernels_fit_four_waves_per_simd(asm):
             continue
         vgpr = int(re.search(r"\.amdhsa_next_free_vgpr\s+(\d+)", body).group(1))
         found.append((name, vgpr))
-    assert len(found) >= 9 + 24, len(found)
-    over = [(n, v) for n, v in found if v > 128]
+    # The instantiations for launches capped at two workgroups per CU
+    # (kWavesPerSimd = 2, "ELi1ELi2E" in the mangled name) may use 256.
+    capped = [(n, v) for n, v in found if "ELi1ELi2E" in n]
+    assert len(capped) >= 6, len(capped)
+    assert len(found) >= 9 + 24 + 6, len(found)
+    over = [(n, v) for n, v in found if v > (256 if "ELi1ELi2E" in n else 128)]
     assert not over, over
