@@ -3,7 +3,8 @@
 // share it, so the probe keeps streaming exactly what the decode streams.
 //
 // Two measured choices (MI355X: 256 CUs in 8 XCDs, cold slot-permuted pools),
-// both taken only for a launch of at least 12 tiles per CU ("large"):
+// both taken only for a "large" launch: at least 8 tiles per CU for 16-bit
+// tiles, 12 for fp32 tiles.
 //
 // * XCD-contiguous tiles. The dispatcher deals consecutive workgroups to the
 //   8 XCDs in turn, so tile order t = blockIdx.x hands each XCD every eighth
@@ -17,9 +18,10 @@
 //   dynamic LDS the kernel does not use. Measured at B = 128 (fp16 pool, cold,
 //   XCD-contiguous), residency cap 2 / 3 / 4 / none: 48.5 / 48.8-49.2 / 49.6 /
 //   49.6 us; the in-place stream probe alone 46.3 / 47.4 / 47.6 / 47.6 us. B =
-//   96: 37.6 / 37.4-37.6 / 38.1 / 38.1 us. Below the threshold the coarser
-//   last round costs more (B = 32: 14.9 -> 16.0 us uncapped vs capped), and
-//   fp32 tiles gain nothing.
+//   96: 37.6 / 37.4-37.6 / 38.1 / 38.1 us. With the decode built for two
+//   waves per SIMD at this cap (gdn_scan.hip), remap + cap 2 against neither:
+//   B = 80 32.4 -> 31.2 us, B = 64 26.2 -> 25.9, B = 48 20.25 -> 20.3, B = 32
+//   13.8 -> 14.8; hence 8 tiles per CU. fp32 tiles gain nothing from the cap.
 //
 // The caller passes overrides for measurement (-1: no override): remap 0 / 1,
 // cap 0 (uncapped) or N > 0. The kernel library takes them from its launch
@@ -61,7 +63,7 @@ inline int env_int(const char* name) {
 // remap_env / cap_env: overrides, -1 for none.
 inline StreamShape stream_shape(long n_tiles, int cus, bool narrow, size_t static_lds,
                                 int remap_env = -1, int cap_env = -1) {
-  const bool large = cus > 0 && n_tiles >= 12L * cus;
+  const bool large = cus > 0 && n_tiles >= (narrow ? 8L : 12L) * cus;
   StreamShape s{0, 0};
   const bool remap = remap_env >= 0 ? remap_env > 0 : large;
   s.xcd_per = (remap && n_tiles % kXcds == 0) ? (int)(n_tiles / kXcds) : 0;

@@ -303,8 +303,9 @@ def test_state_narrowing_rounds_to_nearest_even_exactly(kern, dt):
 @pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16, torch.float32],
                          ids=["f16-pool", "bf16-pool", "f32-pool"])
 def test_launch_shapes_give_identical_bits(kern, dt, H, G):
-    """A launch of at least 12 tiles per CU walks XCD-contiguous tile ranges
-    and, on a 16-bit pool, keeps three workgroups resident per CU. Each tile is
+    """A large launch (at least 8 tiles per CU on a 16-bit pool, 12 on fp32)
+    walks XCD-contiguous tile ranges and, on a 16-bit pool, keeps two
+    workgroups resident per CU (with the two-waves-per-SIMD build). Each tile is
     still one workgroup's work, so every launch shape (forced through the
     override variables) must leave the same pool and y bits; the default one is
     also checked against the oracle on a sample of rows. With H = 12 the tile
