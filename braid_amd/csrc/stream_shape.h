@@ -14,14 +14,17 @@
 //   51.6 -> 49.4, 75.6 -> 72.6, 100.0 -> 93.8 us; fp32 pool at B = 128:
 //   96.9 -> 95.1 us. Up to B = 64 it changes nothing measurable (B = 8 is 2%
 //   slower), hence the threshold. Needs n % 8 == 0.
-// * Two resident workgroups per CU for 16-bit tiles, not four, by asking for
+// * Two resident workgroups per CU, not four, by asking for
 //   dynamic LDS the kernel does not use. Measured at B = 128 (fp16 pool, cold,
 //   XCD-contiguous), residency cap 2 / 3 / 4 / none: 48.5 / 48.8-49.2 / 49.6 /
 //   49.6 us; the in-place stream probe alone 46.3 / 47.4 / 47.6 / 47.6 us. B =
 //   96: 37.6 / 37.4-37.6 / 38.1 / 38.1 us. With the decode built for two
 //   waves per SIMD at this cap (gdn_scan.hip), remap + cap 2 against neither:
 //   B = 80 32.4 -> 31.2 us, B = 64 26.2 -> 25.9, B = 48 20.25 -> 20.3, B = 32
-//   13.8 -> 14.8; hence 8 tiles per CU. fp32 tiles gain nothing from the cap.
+//   13.8 -> 14.8; hence 8 tiles per CU. fp32 tiles (64 KiB, large from 12
+//   tiles per CU) take the cap too: cap 2 / 3 / none at B = 96, 128, 192, 256:
+//   70.0 / 70.5 / 70.9, 91.8 / 92.5 / 93.4, 134.7 / 136.9 / 138.2, 178.1 /
+//   181.6 / 183.3 us.
 //
 // The caller passes overrides for measurement (-1: no override): remap 0 / 1,
 // cap 0 (uncapped) or N > 0. The kernel library takes them from its launch
@@ -67,7 +70,7 @@ inline StreamShape stream_shape(long n_tiles, int cus, bool narrow, size_t stati
   StreamShape s{0, 0};
   const bool remap = remap_env >= 0 ? remap_env > 0 : large;
   s.xcd_per = (remap && n_tiles % kXcds == 0) ? (int)(n_tiles / kXcds) : 0;
-  const int cap = cap_env >= 0 ? cap_env : (large && narrow ? 2 : 0);
+  const int cap = cap_env >= 0 ? cap_env : (large ? 2 : 0);
   if (cap > 0) {
     constexpr long kLdsPerCu = 160 * 1024;
     long pad = kLdsPerCu / cap - (long)static_lds - 1024;
