@@ -246,7 +246,9 @@ __device__ __forceinline__ void store_codes(uint8_t* p, uint2 v) {
 }
 
 // The first grid-stride step's loads are issued before the partials are
-// reduced to the scale, so the reduction overlaps them.
+// reduced to the scale, so the reduction overlaps them: kUnroll vectors a
+// thread when it has that many, else its first vector (a [64, 4096] input
+// gives each thread one).
 template <class Tag>
 __global__ void __launch_bounds__(kThreads)
 quantize(const typename Tag::T* __restrict__ x, const float* __restrict__ partial, int nparts,
@@ -257,9 +259,12 @@ quantize(const typename Tag::T* __restrict__ x, const float* __restrict__ partia
   float o[kUnroll][kVec];
   long j = tid;
   bool full = j + (kUnroll - 1) * stride < nv;
+  const bool one = !full && j < nv;
   if (full) {
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) load_vec(Tag{}, x, (j + u * stride) * kVec, o[u]);
+  } else if (one) {
+    load_vec(Tag{}, x, j * kVec, o[0]);
   }
 
   float m = 0.f;
@@ -280,6 +285,10 @@ quantize(const typename Tag::T* __restrict__ x, const float* __restrict__ partia
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) load_vec(Tag{}, x, (j + u * stride) * kVec, o[u]);
     }
+  }
+  if (one) {
+    store_codes(q + j * kVec, quant_vec(o[0], qs));
+    j += stride;
   }
   for (; j < nv; j += stride) {
     float v1[kVec];
