@@ -3,6 +3,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <cerrno>
 #include <cstdlib>
 #include <vector>
 
@@ -10,20 +11,32 @@ namespace braid {
 
 namespace {
 thread_local std::string g_last_error;
+}  // namespace
+
+int parse_knob(const char* e) {
+  if (e == nullptr || e[0] == '\0') return -1;
+  errno = 0;
+  char* end = nullptr;
+  const long v = std::strtol(e, &end, 10);
+  if (errno != 0 || end == e || *end != '\0' || v < 0 || v > (1L << 30)) return -1;
+  return (int)v;
+}
+
+namespace {
 
 constexpr int kKnobs = 5;
 const char* const kKnobEnv[kKnobs] = {"BRAID_DECODE_XCD_REMAP", "BRAID_DECODE_WGS_PER_CU",
                                       "BRAID_PREFILL_COLS", "BRAID_DECODE_PARTS",
                                       "BRAID_PREFILL_PLAN"};
 
-// Read once, at library load (static initialisation), not per launch.
+// Read once, at library load (static initialisation), not per launch. A value
+// that is not a whole decimal number in [0, 2^30], or is empty, leaves the
+// knob unset (-1), so a typo cannot force a launch shape.
 struct Knobs {
   std::atomic<int> v[kKnobs];
   Knobs() {
-    for (int i = 0; i < kKnobs; ++i) {
-      const char* e = std::getenv(kKnobEnv[i]);
-      v[i].store(e != nullptr && e[0] != '\0' ? std::atoi(e) : -1, std::memory_order_relaxed);
-    }
+    for (int i = 0; i < kKnobs; ++i)
+      v[i].store(parse_knob(std::getenv(kKnobEnv[i])), std::memory_order_relaxed);
   }
 };
 Knobs g_knobs;

@@ -37,8 +37,13 @@ int validate_slots(const int32_t* slot_idx, int B, int64_t n_slots, bool distinc
 // -1 when unset. Initialised once from the environment when the library
 // loads (BRAID_DECODE_XCD_REMAP, BRAID_DECODE_WGS_PER_CU, BRAID_PREFILL_COLS,
 // BRAID_DECODE_PARTS, BRAID_PREFILL_PLAN), then changed only by
-// braid_set_launch_override.
+// braid_set_launch_override. The knobs are process-wide: an override set on
+// one thread shapes the launches of every thread.
 int launch_knob(int knob);
+
+// A knob's value from its environment string: a whole decimal number in
+// [0, 2^30], else -1 (unset): empty, non-numeric, trailing text, negative.
+int parse_knob(const char* e);
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 

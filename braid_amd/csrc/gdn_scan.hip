@@ -11,6 +11,7 @@
 // and :467-551 (prefill); entry-point contracts :313-441 and :553-699.
 #include <algorithm>
 #include <cmath>
+#include <deque>
 #include <functional>
 #include <map>
 #include <mutex>
@@ -950,18 +951,7 @@ int check_act(const void* a_raw, const void* b_raw, int act_dtype, const float* 
 
 // CUs of the current device (0 if the runtime cannot say), cached per device:
 // the decode launch consults it every step.
-int device_cus() {
-  constexpr int kMaxDevices = 64;
-  static std::atomic<int> cached[kMaxDevices];
-  int dev = 0, cus = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 0;
-  if (dev >= 0 && dev < kMaxDevices && (cus = cached[dev].load(std::memory_order_relaxed)) > 0)
-    return cus;
-  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-    return 0;
-  if (dev >= 0 && dev < kMaxDevices) cached[dev].store(cus, std::memory_order_relaxed);
-  return cus;
-}
+int device_cus() { return device_topo().cus; }
 
 // Column parts of a decode launch (gdn_decode_kernel): 2 when a launch has
 // at most as many tiles as the GPU has CUs, else 1. Measured per step on
@@ -982,17 +972,17 @@ void launch_decode_as(void* pool, const int32_t* slot_idx, int B, int H, int G, 
                       int64_t v_row, Gates gates, float* y, int cus, hipStream_t stream) {
   const long n_wg = (long)B * H * P;
   const dim3 grid((unsigned)n_wg), block(tile_threads(kDecodeCols));
+  const DeviceTopo topo = device_topo();
   const StreamShape shape =
-      stream_shape(n_wg, cus, !std::is_same<Tag, F32>::value,
+      stream_shape(n_wg, topo, !std::is_same<Tag, F32>::value,
                    sizeof(TileLds) + kWaves * sizeof(QKLds),
                    launch_knob(BRAID_KNOB_DECODE_XCD_REMAP),
                    launch_knob(BRAID_KNOB_DECODE_WGS_PER_CU));
   // A launch capped at two resident workgroups per CU (its LDS request) takes
   // the two-waves-per-SIMD register budget.
-  constexpr size_t kLdsPerCu = 160 * 1024;
   const size_t lds_per_wg = shape.lds_pad + sizeof(TileLds) + kWaves * sizeof(QKLds);
   if constexpr (P == 1 && !std::is_same<Tag, F32>::value) {
-    if (shape.lds_pad > 0 && kLdsPerCu / lds_per_wg <= 2) {
+    if (shape.lds_pad > 0 && (size_t)topo.lds_per_cu / lds_per_wg <= 2) {
       gdn_decode_kernel<Tag, Gates, P, 2><<<grid, block, shape.lds_pad, stream>>>(
           static_cast<typename Storage<Tag>::T*>(pool), slot_idx, q, k, v, gates, y, H, H / G,
           q_row, k_row, v_row, shape.xcd_per);
@@ -1268,8 +1258,10 @@ int simulate_prefill_plans(const std::vector<int>& lens, int H, int cus);
 
 // Plans already chosen, by (sorted live lengths, H, CUs): a scheduler's ticks
 // repeat their chunk lengths, and a simulation costs 2-95 us of host time
-// (16 ragged rows: 95 us) against about 1 us for the lookup. Bounded: cleared
-// when it reaches kPlanCacheMax entries.
+// (16 ragged rows: 95 us) against about 1 us for the lookup. Bounded: at
+// kPlanCacheMax entries the oldest entry is evicted for each new one (first
+// in, first out), so a serving loop past the bound re-plans only the lengths
+// it has not seen lately instead of all of them at once.
 constexpr size_t kPlanCacheMax = 4096;
 
 int host_prefill_plan(const std::vector<int32_t>& seq_lens, int T, int H, int cus) {
@@ -1278,6 +1270,7 @@ int host_prefill_plan(const std::vector<int32_t>& seq_lens, int T, int H, int cu
   std::sort(lens.begin(), lens.end(), std::greater<int>());
   static std::mutex mu;
   static std::map<std::vector<int>, int> cache;
+  static std::deque<std::map<std::vector<int>, int>::iterator> order;
   std::vector<int> key(lens);
   key.push_back(H);
   key.push_back(cus);
@@ -1288,8 +1281,14 @@ int host_prefill_plan(const std::vector<int32_t>& seq_lens, int T, int H, int cu
   }
   const int plan = simulate_prefill_plans(lens, H, cus);
   std::lock_guard<std::mutex> lock(mu);
-  if (cache.size() >= kPlanCacheMax) cache.clear();
-  cache.emplace(std::move(key), plan);
+  const auto ins = cache.emplace(std::move(key), plan);
+  if (ins.second) {  // another thread may have planned the same lengths meanwhile
+    order.push_back(ins.first);
+    if (order.size() > kPlanCacheMax) {
+      cache.erase(order.front());
+      order.pop_front();
+    }
+  }
   return plan;
 }
 

@@ -890,6 +890,13 @@ __device__ __forceinline__ void normalize_qk_lds(const LM& L, float2 q2, float2 
   buf.q[p1] = q2.y * qi;
   buf.k[p0] = k2.x * ki;
   buf.k[p1] = k2.y * ki;
+  // The reads below take values other lanes of this wave wrote: a wave-scope
+  // release/acquire keeps the compiler from moving them ahead of the writes
+  // (the hardware already completes a wave's LDS operations in order, so this
+  // emits no wait of its own).
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   const int base = (L.w * kRowGroups + L.rg) * kRowsPerLane;
   loadN<kRowsPerLane>(&buf.q[base], out.qh);
   loadN<kRowsPerLane>(&buf.k[base], out.kh);

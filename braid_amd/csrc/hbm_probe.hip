@@ -106,15 +106,11 @@ int braid_probe_stream(int kind, void* base, int64_t n_tiles, const int32_t* til
   hipStream_t s = static_cast<hipStream_t>(stream);
   // The decode's launch shape for the same tile count (the decode's 16-bit
   // tiles hold its exchange buffer, 4,104 bytes of static LDS).
-  int dev = 0, cus = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-    cus = 0;
   // The decode's overrides, read once from the environment as the kernel
   // library reads them.
   static const int remap_env = braid::env_int("BRAID_DECODE_XCD_REMAP");
   static const int cap_env = braid::env_int("BRAID_DECODE_WGS_PER_CU");
-  const braid::StreamShape sh = braid::stream_shape(n_tiles, cus, true, 4104, remap_env, cap_env);
+  const braid::StreamShape sh = braid::stream_shape(n_tiles, braid::device_topo(), true, 4104, remap_env, cap_env);
   if (kind == 0)
     probe_rmw<<<grid, block, sh.lds_pad, s>>>(static_cast<char*>(base), tile_idx,
                                               sh.xcd_per);

@@ -26,6 +26,10 @@
 //   70.0 / 70.5 / 70.9, 91.8 / 92.5 / 93.4, 134.7 / 136.9 / 138.2, 178.1 /
 //   181.6 / 183.3 us.
 //
+// The device's CU count, XCD count and LDS per CU come from its HIP
+// attributes (device_topo), so a partitioned device gets its own figures:
+// dispatch order where it has another XCD count, the cap sized to its LDS.
+//
 // The caller passes overrides for measurement (-1: no override): remap 0 / 1,
 // cap 0 (uncapped) or N > 0. The kernel library takes them from its launch
 // knobs, which are read from the environment once, when the library loads,
@@ -39,6 +43,7 @@
 
 namespace braid {
 
+// The XCD count the remap below is written for (MI355X: 256 CUs in 8 XCDs).
 constexpr int kXcds = 8;
 
 // The tile a workgroup streams (see above): `per` = tiles per XCD (n / 8)
@@ -50,30 +55,72 @@ __device__ __forceinline__ int stream_tile(int per) {
   return per > 0 ? remapped : (int)blockIdx.x;
 }
 
+// What the launch shape needs to know of the current device, from its HIP
+// attributes (not assumed): CUs, XCDs (XCCs) and LDS bytes per CU. A
+// partitioned MI355X (e.g. one XCD per logical device) reports its own
+// partition's figures. Zeros when a query fails: no large-launch choices.
+struct DeviceTopo {
+  int cus = 0;
+  int xcds = 0;
+  long lds_per_cu = 0;
+};
+
+// Queried once per device ordinal (the attributes do not change while the
+// process runs) with that device current.
+inline DeviceTopo device_topo() {
+  constexpr int kMaxDevices = 64;
+  static DeviceTopo cached[kMaxDevices];
+  static bool known[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return DeviceTopo{};
+  if (dev >= 0 && dev < kMaxDevices && __atomic_load_n(&known[dev], __ATOMIC_ACQUIRE))
+    return cached[dev];
+  DeviceTopo t;
+  int v = 0;
+  if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
+    t.cus = v;
+  v = 0;
+  if (hipDeviceGetAttribute(&v, hipDeviceAttributeNumberOfXccs, dev) == hipSuccess) t.xcds = v;
+  v = 0;
+  if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) ==
+      hipSuccess)
+    t.lds_per_cu = v;
+  if (dev >= 0 && dev < kMaxDevices) {
+    cached[dev] = t;  // racing writers store the same values
+    __atomic_store_n(&known[dev], true, __ATOMIC_RELEASE);
+  }
+  return t;
+}
+
 struct StreamShape {
   int xcd_per;  // argument of stream_tile
   size_t lds_pad;      // dynamic LDS bytes to request
 };
 
-// An integer from the environment, or -1 when the variable is unset.
+// A non-negative integer from the environment, or -1 when the variable is
+// unset, empty or not a whole decimal number.
 inline int env_int(const char* name) {
   const char* e = getenv(name);
-  return e ? atoi(e) : -1;
+  if (e == nullptr || e[0] == '\0') return -1;
+  char* end = nullptr;
+  const long v = strtol(e, &end, 10);
+  return (end == e || *end != '\0' || v < 0 || v > (1L << 30)) ? -1 : (int)v;
 }
 
-// cus: CUs of the device (0 if unknown: no large-launch choices);
-// narrow: 16-bit tiles; static_lds: the kernel's own LDS bytes;
-// remap_env / cap_env: overrides, -1 for none.
-inline StreamShape stream_shape(long n_tiles, int cus, bool narrow, size_t static_lds,
-                                int remap_env = -1, int cap_env = -1) {
-  const bool large = cus > 0 && n_tiles >= (narrow ? 8L : 12L) * cus;
+// topo: the device (cus 0: no large-launch choices); narrow: 16-bit tiles;
+// static_lds: the kernel's own LDS bytes; remap_env / cap_env: overrides, -1
+// for none. The XCD remap is taken only on a device with kXcds XCDs (the
+// order stream_tile computes); the residency cap divides the device's own
+// LDS per CU.
+inline StreamShape stream_shape(long n_tiles, const DeviceTopo& topo, bool narrow,
+                                size_t static_lds, int remap_env = -1, int cap_env = -1) {
+  const bool large = topo.cus > 0 && n_tiles >= (narrow ? 8L : 12L) * topo.cus;
   StreamShape s{0, 0};
-  const bool remap = remap_env >= 0 ? remap_env > 0 : large;
+  const bool remap = remap_env >= 0 ? remap_env > 0 : (large && topo.xcds == kXcds);
   s.xcd_per = (remap && n_tiles % kXcds == 0) ? (int)(n_tiles / kXcds) : 0;
-  const int cap = cap_env >= 0 ? cap_env : (large ? 2 : 0);
-  if (cap > 0) {
-    constexpr long kLdsPerCu = 160 * 1024;
-    long pad = kLdsPerCu / cap - (long)static_lds - 1024;
+  const int cap = cap_env >= 0 ? cap_env : (large && topo.lds_per_cu > 0 ? 2 : 0);
+  if (cap > 0 && topo.lds_per_cu > 0) {
+    long pad = topo.lds_per_cu / cap - (long)static_lds - 1024;
     if (pad > 65536) pad = 65536;
     s.lds_pad = pad > 0 ? (size_t)pad : 0;
   }

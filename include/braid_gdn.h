@@ -66,7 +66,10 @@ const char* braid_last_error(void);
  *                                eighth layout, the next n4 quarter, the next n2
  *                                split
  *
- * A captured graph keeps the launch shape it was captured with.
+ * A captured graph keeps the launch shape it was captured with. An environment
+ * value that is not a whole decimal number in [0, 2^30] leaves the knob unset.
+ * The knobs are process-wide: an override set on one thread shapes the
+ * launches of every thread.
  */
 enum braid_launch_knob {
   BRAID_KNOB_DECODE_XCD_REMAP = 0,
@@ -264,9 +267,11 @@ int braid_quantize_act(const void* x, int x_dtype, int64_t n, uint8_t* q,
  * and needs no caller buffer beyond x, q and scale. No counterpart in the
  * reference: it is for callers that cannot allocate, such as code under
  * graph capture or a serving loop that forbids allocation. Codes and scale
- * equal braid_quantize_act's bit for bit. Every call on one GPU shares that
- * GPU's scratch, so calls that overlap on one GPU (different streams, or
- * different threads) race and must be serialised by the caller; a call fully
+ * equal braid_quantize_act's bit for bit. Single-stream contract: every call
+ * on one GPU shares that GPU's scratch, so the caller issues all of a GPU's
+ * calls on one stream (or otherwise orders them, e.g. with events); calls
+ * that overlap on one GPU (different streams, or different threads) race and
+ * may return wrong codes and scales. The library does not detect this. A call fully
  * rewrites the partials it reads, so nothing needs clearing between calls.
  * The partial count never exceeds the scratch for any n (it is capped at
  * 1024); a larger count would be rejected with BRAID_EINVAL. Arguments and

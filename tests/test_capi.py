@@ -204,3 +204,77 @@ def test_host_prefill_plan_picks_the_measured_plans(lib):
     assert lib.braid_prefill_plan(zeros, 3, 10, 32, 256) == 0
     assert lib.braid_prefill_plan(None, 3, 10, 32, 256) == -1
     assert "host lengths" in _err(lib)
+
+
+def _plan(lib, lens, T=None, H=32, cus=256):
+    arr = (ctypes.c_int32 * len(lens))(*lens)
+    p = lib.braid_prefill_plan(arr, len(lens), T if T is not None else max(max(lens), 1), H, cus)
+    assert p >= 0, _err(lib)
+    return p >> 20, (p >> 10) & 1023, p & 1023
+
+
+def test_host_prefill_plan_edge_cases(lib):
+    """The host planner's invariants, away from the measured batches: a plan
+    never upgrades more rows than it has live ones (or more than its tier
+    limits: n8 <= 2, n4 <= 6, n2 <= 8); it depends only on the multiset of
+    live lengths (order and lengths clipped to T); a single live row among
+    empty ones runs the eighth layout, as a batch of one does; all-equal rows
+    at every CU's two slots plan nothing; B at the planned kernel's row cap
+    (1024) plans in bounded host time."""
+    import random
+    import time
+
+    rng = random.Random(7)
+    for _ in range(40):
+        B = rng.randint(1, 40)
+        lens = [rng.choice([0, rng.randint(1, 1024)]) for _ in range(B)]
+        n8, n4, n2 = _plan(lib, lens, T=1024)
+        live = sum(1 for x in lens if x > 0)
+        assert n8 <= 2 and n4 <= 6 and n2 <= 8
+        assert n8 + n4 + n2 <= max(live, 0) or (live == 0 and (n8, n4, n2) == (0, 0, 0)), lens
+        shuffled = lens[:]
+        rng.shuffle(shuffled)
+        assert _plan(lib, shuffled, T=1024) == (n8, n4, n2)
+    # clipping to T: lengths beyond T plan as T
+    assert _plan(lib, [5000, 300], T=1000) == _plan(lib, [1000, 300], T=1000)
+    # one live row among empty ones: the same as that row alone
+    assert _plan(lib, [0, 0, 700, 0]) == _plan(lib, [700]) == (1, 0, 0)
+    # sixteen equal rows fill 512 workgroup slots whole: nothing to upgrade
+    assert _plan(lib, [256] * 16) == (0, 0, 0)
+    # the row cap: 1024 rows, distinct lengths (no cache hit), bounded time
+    lens = [1 + (i * 37) % 97 for i in range(1024)]
+    t0 = time.perf_counter()
+    n8, n4, n2 = _plan(lib, lens)
+    assert time.perf_counter() - t0 < 2.0
+    assert n8 <= 2 and n4 <= 6 and n2 <= 8
+
+
+def test_host_prefill_plan_cache_evicts_one_at_a_time(lib):
+    """Past its bound (4096 length sets) the plan cache evicts its oldest
+    entries, not everything: plans stay what the simulation gives for any
+    history of calls."""
+    first = _plan(lib, [454, 610, 334, 542, 393, 861, 814, 65])
+    for i in range(4200):
+        _plan(lib, [100 + i % 900, 50 + i // 900, 7], T=2048)
+    assert _plan(lib, [454, 610, 334, 542, 393, 861, 814, 65]) == first == (0, 1, 6)
+
+
+def test_launch_knobs_ignore_malformed_environment_values():
+    """A launch knob's environment value counts only when it is a whole
+    decimal number in [0, 2^30]; anything else leaves the knob unset (-1), so
+    a typo cannot force a launch shape. Checked in a fresh process, since the
+    knobs are read once when the library loads."""
+    import os
+    import subprocess
+    import sys
+
+    code = (
+        "import ctypes, sys; from braid_amd.kernels import loader; "
+        "lib = ctypes.CDLL(str(loader.LIB_PATH)); "
+        "print(' '.join(str(lib.braid_get_launch_override(i)) for i in range(5)))"
+    )
+    env = dict(os.environ, BRAID_DECODE_XCD_REMAP="abc", BRAID_DECODE_WGS_PER_CU="2x",
+               BRAID_PREFILL_COLS="", BRAID_DECODE_PARTS="-2", BRAID_PREFILL_PLAN="1025")
+    out = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True,
+                         cwd=str(Path(__file__).resolve().parents[1]), check=True)
+    assert out.stdout.split() == ["-1", "-1", "-1", "-1", "1025"], out.stdout + out.stderr
