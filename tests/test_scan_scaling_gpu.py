@@ -5,7 +5,8 @@ Cold residency throughout, as there: step i uses its own distinct slots of
 one pool larger than 1 GiB, so no state is L2/MALL-resident when it is
 revisited (a pool sized to the batch would report above-HBM figures). Each
 measurement replays a captured graph of back-to-back launches and times it
-with events. The roofline is the measured in-place stream of the same state
+between two GPU clock stamps inside the graph, as bench.py does. The roofline
+is the measured in-place stream of the same state
 tiles (libbraid_probe.so, the decode's lane layout with no arithmetic): the
 ceiling this box gives the access pattern, not the 8 TB/s datasheet figure.
 """
@@ -28,25 +29,20 @@ ROW_BYTES = 2 * H * D * D * 2 + (2 * G * D + 2 * H * D) * 4 + H * 2 * 2 + 4
 
 
 def _graph_seconds(fn, launches):
+    """Seconds per launch: `launches` back-to-back calls captured in one graph
+    between two GPU clock stamps (bench.py's method), median of 5 replays. The
+    graph's own launch latency stays outside the stamps."""
+    import bench
+
     for i in range(3):
         fn(i)
     torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        for i in range(launches):
-            fn(i)
+    clock = bench.GpuClock(torch)
+    graph = bench.capture_clocked(torch, clock, lambda: [fn(i) for i in range(launches)])
     graph.replay()
     torch.cuda.synchronize()
-    times = []
-    for _ in range(5):
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
-        graph.replay()
-        b.record()
-        torch.cuda.synchronize()
-        times.append(a.elapsed_time(b) / 1e3 / launches)
-    times.sort()
-    return times[len(times) // 2]
+    times = sorted(bench.replay_times(torch, graph, 5, clock))
+    return times[len(times) // 2] / launches
 
 
 @pytest.fixture(scope="module")
