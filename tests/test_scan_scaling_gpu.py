@@ -13,6 +13,7 @@ ceiling this box gives the access pattern, not the 8 TB/s datasheet figure.
 from __future__ import annotations
 
 import ctypes
+import time
 
 import pytest
 import torch
@@ -30,8 +31,9 @@ ROW_BYTES = 2 * H * D * D * 2 + (2 * G * D + 2 * H * D) * 4 + H * 2 * 2 + 4
 
 def _graph_seconds(fn, launches):
     """Seconds per launch: `launches` back-to-back calls captured in one graph
-    between two GPU clock stamps (bench.py's method), median of 5 replays. The
-    graph's own launch latency stays outside the stamps."""
+    between two GPU clock stamps (bench.py's method), median of 5 replays
+    after 20 ms of warm replays. The graph's own launch latency stays outside
+    the stamps."""
     import bench
 
     for i in range(3):
@@ -39,8 +41,12 @@ def _graph_seconds(fn, launches):
     torch.cuda.synchronize()
     clock = bench.GpuClock(torch)
     graph = bench.capture_clocked(torch, clock, lambda: [fn(i) for i in range(launches)])
-    graph.replay()
-    torch.cuda.synchronize()
+    # replays for at least 20 ms first: the first replays after other work
+    # run measurably slower
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < 0.02:
+        graph.replay()
+        torch.cuda.synchronize()
     times = sorted(bench.replay_times(torch, graph, 5, clock))
     return times[len(times) // 2] / launches
 
