@@ -356,6 +356,29 @@ __device__ __forceinline__ float add_xor32(float v) {
   return __uint_as_float(p[0]) + __uint_as_float(p[1]);
 }
 
+// The same partner sums where only the lower lanes of each pair consume the
+// result: lanes of even 16-lane rows (xor 16) or of the lower 32 lanes (xor
+// 32) end with v + partner, the same addition in the same operand order as
+// add_xor16 / add_xor32, so the same bits there; the other lanes hold
+// garbage. The swap's second operand is a don't-care register, so the
+// compiler need not copy v into it first (each full-wave swap of v with
+// itself costs a v_mov and a wait state).
+// A register with no defined value: an empty asm that "writes" it, so the
+// compiler emits nothing to set it (a poison value would be set to 0).
+__device__ __forceinline__ uint32_t dont_care() {
+  uint32_t x;
+  asm volatile("" : "=v"(x));
+  return x;
+}
+__device__ __forceinline__ float add_xor16_lo(float v) {
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), dont_care(), false, false);
+  return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+__device__ __forceinline__ float add_xor32_lo(float v) {
+  const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), dont_care(), false, false);
+  return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+
 // Sum over all 64 lanes: stages xor 1, 2, 4, 8, 16, 32.
 __device__ __forceinline__ float wave_sum(float v) {
   return add_xor32(add_xor16(add_xor8(add_xor4(add_xor2(add_xor1(v))))));
@@ -365,7 +388,10 @@ __device__ __forceinline__ float wave_sum(float v) {
 // v + (lane xor 16), then + (lane xor 32). kPermlane: through the permlane
 // swaps (VALU); otherwise through ds_bpermute, which holds no extra registers
 // (the fused conv + decode kernels have none to spare at 128 VGPRs). Same
-// sums either way (a + b == b + a), so the same bits.
+// sums either way (a + b == b + a), so the same bits. (The lower-lanes
+// variants add_xor*_lo would do here too, since only row group 0 stores the
+// totals; measured on the B = 128 decode they gained nothing, 47.96 -> 48.00
+// us, so the full-wave swaps stay.)
 template <bool kPermlane = false>
 __device__ __forceinline__ float rowgroup_sum(float v) {
   if constexpr (kPermlane) return add_xor32(add_xor16(v));
@@ -800,6 +826,11 @@ struct ScanLayoutOf<8> {
 __device__ __forceinline__ float scan_column_sum(float c0, float c1, float c2, float c3) {
   return add_xor32(add_xor16((c0 + c1) + (c2 + c3)));
 }
+// The same total, valid only in row block 0's lanes (lanes 0-15, the ones
+// that store y).
+__device__ __forceinline__ float scan_column_sum_row0(float c0, float c1, float c2, float c3) {
+  return add_xor32_lo(add_xor16_lo((c0 + c1) + (c2 + c3)));
+}
 
 // Cross-wave exchange buffers for one tile: per-row-block column partials of
 // kv and of y, kept apart so one token's y exchange never overwrites kv
@@ -1059,7 +1090,7 @@ __device__ __forceinline__ void scan_token(Row<Tag, CPL> (&S)[kRowGroups][kRowsP
   }
 #pragma unroll
   for (int c = 0; c < CPL; ++c)
-    y[c] = scan_column_sum(ch[0][c], ch[1][c], ch[2][c], ch[3][c]) * kYScale;
+    y[c] = scan_column_sum_row0(ch[0][c], ch[1][c], ch[2][c], ch[3][c]) * kYScale;
 }
 
 // The one-column layout's token over row pairs: P[p][i] holds rows of row
@@ -1099,7 +1130,7 @@ __device__ __forceinline__ void scan_token_pairs(RowPair1<Tag> (&P)[2][kRowsPerL
         ch[2 * p + h] = fmaf(n[h], qh[2 * p + h + kRowGroups * i], ch[2 * p + h]);
     }
   }
-  y = scan_column_sum(ch[0], ch[1], ch[2], ch[3]) * kYScale;
+  y = scan_column_sum_row0(ch[0], ch[1], ch[2], ch[3]) * kYScale;
 }
 
 // One token of the quarter layout on this lane's 16 rows x 1 column: S[rgl][i]
@@ -1134,7 +1165,7 @@ __device__ __forceinline__ void scan_token_quarter(RowPair1<Tag> (&P)[kRowsPerLa
 #pragma unroll
     for (int g = 0; g < 2; ++g) ch[g] = fmaf(n[g], qh[g][i], ch[g]);
   }
-  y = add_xor32(add_xor16(add_xor8(ch[0] + ch[1]))) * kYScale;
+  y = add_xor32_lo(add_xor16_lo(add_xor8(ch[0] + ch[1]))) * kYScale;
 }
 
 // One token of the eighth layout on this lane's chain of 8 rows x 1 column:
