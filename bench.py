@@ -195,9 +195,10 @@ def time_steps(torch, kern, work, steps, warmup, reps=31):
     """Capture `steps` decode launches (step i on pool i % P) in one graph,
     bracketed by GPU clock stamps, and replay it `reps` times, each replay
     timed alone (the reference's measure_graphed, braid/bench/noise_floor.py
-    :52-105, on the GPU's clock). Returns the median seconds for the `steps`
-    launches and the per-step spread, with the event-timed figure of the same
-    replays (graph launch latency included) beside it."""
+    :52-105, on the GPU's clock), after 50 ms of untimed replays. Returns the
+    median seconds for the `steps` launches and the per-step spread, with the
+    event-timed figure of the same replays (graph launch latency included)
+    beside it."""
     pools, slot_maps, inputs, A, dtb = work
     P = len(pools)
     clock = GpuClock(torch)
@@ -212,8 +213,15 @@ def time_steps(torch, kern, work, steps, warmup, reps=31):
         launch(i)
     torch.cuda.synchronize()
     graph = capture_clocked(torch, clock, lambda: [launch(i) for i in range(steps)])
-    graph.replay()                       # untimed: first replay uploads the graph
-    torch.cuda.synchronize()
+    # Untimed replays for at least 50 ms first (the first uploads the graph):
+    # the first replays after other work run measurably slower, and with a
+    # short graph (K = 20 is about 1 ms) they would set the upper percentiles.
+    warm = time.perf_counter()
+    n_warm = 0
+    while n_warm < 2 or time.perf_counter() - warm < 0.05:
+        graph.replay()
+        torch.cuda.synchronize()
+        n_warm += 1
     times = replay_times(torch, graph, reps, clock)
     ev = sorted(replay_times(torch, graph, 11))
     first = times[0]
