@@ -330,6 +330,39 @@ def test_both_scan_layouts_are_decode_bit_for_bit(kern, dt, cols):
     assert bool(same.all()), f"states differ by {(pc.float() - ps.float()).abs().max().item():.3e}"
 
 
+@pytest.mark.parametrize("cols", [1, 2, 0, 4, 8],
+                         ids=["split-1col", "whole-2col", "planned", "quarter", "eighth"])
+def test_stage_boundaries_are_decode_bit_for_bit(kern, cols):
+    """Row lengths around the 32-token stage and the token-pair loops' tails:
+    33 (a second stage of one token), 64 (two full stages), 34 and 35 (a
+    second stage of a pair, and of a pair and one), 1 and 31 (one stage, a
+    single token / an odd tail). Each layout must equal decode applied token
+    by token, bit for bit, with zeros at the pad outputs."""
+    lens_l = [33, 64, 34, 1, 35, 31]
+    B, T, H, G = len(lens_l), max(lens_l), 32, 16
+    inp = prefill_inputs(B, T, H=H, G=G, seed=91)
+    a, b, A, dtb = raw_gates((B, T, H), H, torch.bfloat16, seed=92)
+    lens = torch.tensor(lens_l, dtype=torch.int32, device=DEV)
+    slots = torch.tensor([7, 2, 0, 5, 3, 8], dtype=torch.int32, device=DEV)
+    pc = pool(10, H=H, dtype=torch.float16)
+    ps = pc.clone()
+    yc = torch.empty(B, T, H, 128, device=DEV)
+    with kern.launch_override(prefill_layout=cols):
+        kern.gdn_prefill_raw(pc, slots, inp["q"], inp["k"], inp["v"], a, b, A, dtb, yc, lens)
+    for t in range(T):
+        live = (t < lens).nonzero().flatten()
+        yt = torch.empty(live.numel(), H, 128, device=DEV)
+        kern.gdn_decode_raw(ps, slots[live].contiguous(), inp["q"][live, t].contiguous(),
+                            inp["k"][live, t].contiguous(), inp["v"][live, t].contiguous(),
+                            a[live, t].contiguous(), b[live, t].contiguous(), A, dtb, yt)
+        assert torch.equal(yc[live, t], yt), f"token {t}: outputs differ"
+        dead = (t >= lens).nonzero().flatten()
+        assert bool((yc[dead, t] == 0).all()), f"token {t}: pad outputs are not 0"
+    torch.cuda.synchronize()
+    same = (pc == ps) | (pc.isnan() & ps.isnan())
+    assert bool(same.all()), f"states differ by {(pc.float() - ps.float()).abs().max().item():.3e}"
+
+
 @pytest.mark.parametrize("dt", POOL_DTYPES, ids=POOL_IDS)
 def test_a_plan_with_every_tier_is_decode_bit_for_bit(kern, dt):
     """A planned launch forced to use all four tiers (the longest row in the
