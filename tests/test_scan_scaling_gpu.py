@@ -119,3 +119,16 @@ def test_large_batches_reach_the_stream_roofline(curve):
 def test_l2_cliff_is_not_catastrophic(curve):
     """Per-row cost must not jump from one row to two (:83-98)."""
     assert curve[2]["seconds"] / 2 < 1.5 * curve[1]["seconds"]
+
+
+def test_box_copy_bandwidth_is_sane():
+    """The box itself, as the reference's tests/test_env.py:17-36 gates its own
+    (> 1,200 GB/s on the RTX 5090): a 1 GiB torch device-to-device copy must
+    move more than 3,000 GB/s (read + write) on an MI355X, which measures
+    4.8-5.2 TB/s. A slower box would make every bandwidth figure here
+    meaningless, so the suite says so first."""
+    import bench
+
+    gbs = bench.copy_bandwidth(torch)
+    print(f"\n1 GiB torch copy: {gbs:.0f} GB/s")
+    assert gbs > 3000.0, gbs
