@@ -710,13 +710,18 @@ __device__ __forceinline__ void store_row(const Row<Tag, CPL>& r, const LaneMap<
 // Lane geometry of the scan (prefill) layout: a lane holds all 32 rows of its
 // row block w for CPL columns, so the row-group level of every column sum is
 // done in-lane and a column sum crosses lanes only over the four row blocks.
-// Lane bits: 0-3 column chunk cc, 4-5 row block w; a wave owns 16 * CPL whole
+// Lane bits: 0-1 row block w, 2-5 column chunk cc; a wave owns 16 * CPL whole
 // columns, so a token needs no workgroup barrier. The lane's rows are indexed
 // (rg, i) -> w * 32 + rg + 4 i as in the decode layout, so its four in-lane
 // chains are the decode chains of row groups 0..3, combined as
 // (rg0 + rg1) + (rg2 + rg3) like the decode's lane-xor-16 / xor-32 stages, and
 // the row blocks as (w0 + w1) + (w2 + w3) like the decode's LDS tree: every
-// sum has the decode's bits.
+// sum has the decode's bits. The row blocks sit in the low lane bits so that
+// their two stages are DPP quad permutes (lane xor 1, xor 2) rather than
+// permlane swaps across 16 and 32 lanes: a token's kv total is on the scan's
+// critical path, and a quad permute is both shorter and one instruction
+// (config 4's 4 x 256 tokens 0.1233 -> 0.1203 ms, one 512-token row
+// 0.241 -> 0.228 ms; the same bits).
 //
 // A workgroup is four waves. With two columns per lane they own the tile's
 // 128 columns; with one column per lane (kParts = 2) a tile is two
@@ -735,8 +740,8 @@ struct ScanMap {
   __device__ __forceinline__ ScanMap(int tid, int part) {
     lane = tid & 63;
     wave = tid >> 6;
-    cc = lane & 15;
-    w = lane >> 4;
+    cc = lane >> 2;
+    w = lane & 3;
     col0 = (part * kWaves + wave) * kColsPerWave + cc * CPL;
   }
   __device__ __forceinline__ int row(int rg, int i) const {
@@ -822,14 +827,10 @@ struct ScanLayoutOf<8> {
 };
 
 // Column total of the scan layout from a lane's four row-group chains:
-// (rg0 + rg1) + (rg2 + rg3) in-lane, then (w0 + w1) + (w2 + w3) across lanes.
+// (rg0 + rg1) + (rg2 + rg3) in-lane, then (w0 + w1) + (w2 + w3) across the
+// lanes of a quad (lane xor 1, then xor 2).
 __device__ __forceinline__ float scan_column_sum(float c0, float c1, float c2, float c3) {
-  return add_xor32(add_xor16((c0 + c1) + (c2 + c3)));
-}
-// The same total, valid only in row block 0's lanes (lanes 0-15, the ones
-// that store y).
-__device__ __forceinline__ float scan_column_sum_row0(float c0, float c1, float c2, float c3) {
-  return add_xor32_lo(add_xor16_lo((c0 + c1) + (c2 + c3)));
+  return add_xor2(add_xor1((c0 + c1) + (c2 + c3)));
 }
 
 // Cross-wave exchange buffers for one tile: per-row-block column partials of
@@ -1090,7 +1091,7 @@ __device__ __forceinline__ void scan_token(Row<Tag, CPL> (&S)[kRowGroups][kRowsP
   }
 #pragma unroll
   for (int c = 0; c < CPL; ++c)
-    y[c] = scan_column_sum_row0(ch[0][c], ch[1][c], ch[2][c], ch[3][c]) * kYScale;
+    y[c] = scan_column_sum(ch[0][c], ch[1][c], ch[2][c], ch[3][c]) * kYScale;
 }
 
 // The one-column layout's token over row pairs: P[p][i] holds rows of row
@@ -1130,7 +1131,7 @@ __device__ __forceinline__ void scan_token_pairs(RowPair1<Tag> (&P)[2][kRowsPerL
         ch[2 * p + h] = fmaf(n[h], qh[2 * p + h + kRowGroups * i], ch[2 * p + h]);
     }
   }
-  y = scan_column_sum_row0(ch[0], ch[1], ch[2], ch[3]) * kYScale;
+  y = scan_column_sum(ch[0], ch[1], ch[2], ch[3]) * kYScale;
 }
 
 // One token of the quarter layout on this lane's 16 rows x 1 column: S[rgl][i]
