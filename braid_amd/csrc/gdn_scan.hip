@@ -299,12 +299,33 @@ gdn_conv_decode_kernel_f32(float* __restrict__ pool, float* __restrict__ conv_po
 
 // A prefill stage: the next kStage tokens' per-token inputs, staged in LDS by
 // a parallel prologue so that the serial loop reads nothing from global memory:
-//   qk   normalised q and k (q_hat, k_hat), each [kSS] in row order;
+//   qk   normalised q and k (q_hat, k_hat), each kStageVec floats holding the
+//        kSS rows in the order the launch's layout reads them (StageOrder);
 //   v    the value row [kHD];
 //   gate alpha, beta.
 constexpr int kStage = 32;
+
+// Where row r of q_hat / k_hat sits in a stage vector, per layout:
+//   kRowOrder      r (the whole and split layouts read 32-row blocks);
+//   kEighthOrder   qk_lds_pos(r): an eighth-layout lane's chain of eight rows
+//                  is eight consecutive floats;
+//   kQuarterOrder  a quarter-layout lane's 16 rows (row block w, row groups
+//                  2 rgh and 2 rgh + 1) are 16 consecutive floats, (i, rgl)
+//                  at 2 i + rgl, in groups of kQuarterGroup floats: the group
+//                  stride of 20 (not 16) puts the eight groups a read touches
+//                  on distinct LDS banks. Four 16-byte reads per vector instead
+//                  of eight 8-byte pairs (quarter-layout tokens: config 4's
+//                  4 x 256 0.1255 -> 0.120 ms, one 512-token row 0.161 ->
+//                  0.155 ms; the same bits).
+enum StageOrder { kRowOrder, kEighthOrder, kQuarterOrder };
+constexpr int kQuarterGroup = 20;
+constexpr int kStageVec = 8 * kQuarterGroup;  // >= kSS
+__device__ __forceinline__ int quarter_stage_pos(int w, int rgh, int i, int rgl) {
+  return (w * 2 + rgh) * kQuarterGroup + 2 * i + rgl;
+}
+
 struct alignas(16) StageLds {
-  float qk[kStage][2][kSS];
+  float qk[kStage][2][kStageVec];
   float v[kStage][kHD];
   float gate[kStage][2];
 };
@@ -371,10 +392,8 @@ __device__ __forceinline__ void load_stage(StageRegs<kTileWaves>& r, int wave, i
 // a third of the instructions (one 16-lane row per vector: four vectors per
 // wave instruction, and no exchange across rows).
 //
-// kLaneOrder (the eighth layout): q_hat and k_hat go to LDS in the order its
-// lanes read them, row r at qk_lds_pos(r), so a lane's eight rows (one chain)
-// are eight consecutive floats.
-template <int kTileWaves, bool kLaneOrder, class Gates>
+// kOrder: where each row of q_hat and k_hat goes in LDS (StageOrder).
+template <int kTileWaves, StageOrder kOrder, class Gates>
 __device__ __forceinline__ void write_stage(const StageRegs<kTileWaves>& r, int wave, int lane,
                                             const Gates& gates, const GateConst& gc, int n,
                                             StageLds& st) {
@@ -415,7 +434,17 @@ __device__ __forceinline__ void write_stage(const StageRegs<kTileWaves>& r, int 
       const float fu = rsqrtf(f[u] + kL2Eps);
       const float4 a = r.qk[u][0], b = r.qk[u][1];
       float* dst = &st.qk[j][c][0];
-      if constexpr (kLaneOrder) {
+      if constexpr (kOrder == kQuarterOrder) {
+        // Rows e0 + k (e0 a multiple of 8): row block e0 / 32, row group k % 4,
+        // chain index (e0 % 32) / 4 + k / 4.
+        const int wb = e0 >> 5, i0 = (e0 & 31) >> 2;
+        const float xs[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk) {
+          const int rg = kk & 3;
+          dst[quarter_stage_pos(wb, rg >> 1, i0 + (kk >> 2), rg & 1)] = xs[kk] * fu;
+        }
+      } else if constexpr (kOrder == kEighthOrder) {
         // Rows e0 + k (e0 a multiple of 8): row block e0 / 32, row group k % 4,
         // chain index (e0 / 4) % 8 + k / 4.
         const int base = (e0 >> 5) * (kRowGroups * kRowsPerLane) + ((e0 >> 2) & 7);
@@ -469,27 +498,31 @@ __device__ __forceinline__ void read_token(const StageLds& st, int j, int r0, in
   }
 }
 
-// The quarter layout's token: its 16 rows' k_hat / q_hat (rows r0 + 2 rgh +
-// rgl + 4 i: a float2 per i), its column's v, and the gates.
+// The quarter layout's token: its 16 rows' k_hat / q_hat (rows w * 32 + 2 rgh +
+// rgl + 4 i, consecutive in the stage's quarter order from `pos`), its
+// column's v, and the gates.
 struct TokenInQ {
   float kh[2][kRowsPerLane], qh[2][kRowsPerLane];
   float v, alpha, beta;
 };
 
-__device__ __forceinline__ void read_token_quarter(const StageLds& st, int j, int r0, int col0,
+__device__ __forceinline__ void read_token_quarter(const StageLds& st, int j, int pos, int col0,
                                                    TokenInQ& t) {
   const float2 ab = *reinterpret_cast<const float2*>(&st.gate[j][0]);
   t.alpha = ab.x;
   t.beta = ab.y;
   t.v = st.v[j][col0];
+  // Four 16-byte reads per vector (a group is 16-byte aligned, not 64).
 #pragma unroll
-  for (int i = 0; i < kRowsPerLane; ++i) {
-    const float2 k2 = *reinterpret_cast<const float2*>(&st.qk[j][1][r0 + kRowGroups * i]);
-    const float2 q2 = *reinterpret_cast<const float2*>(&st.qk[j][0][r0 + kRowGroups * i]);
-    t.kh[0][i] = k2.x;
-    t.kh[1][i] = k2.y;
-    t.qh[0][i] = q2.x;
-    t.qh[1][i] = q2.y;
+  for (int p = 0; p < kRowsPerLane / 2; ++p) {
+    float k4[4], q4[4];
+    loadN<4>(&st.qk[j][1][pos + 4 * p], k4);
+    loadN<4>(&st.qk[j][0][pos + 4 * p], q4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      t.kh[e & 1][2 * p + (e >> 1)] = k4[e];
+      t.qh[e & 1][2 * p + (e >> 1)] = q4[e];
+    }
   }
 }
 
@@ -629,10 +662,10 @@ __device__ __forceinline__ void prefill_tile(typename Storage<Tag>::T* __restric
   S.load(L, tile);
 
   constexpr int kW = LM::kWaves;
-  // The lane's first row: its row block's (and, in the quarter layout, its
-  // row-group half's).
+  // Where the lane's rows start in a stage vector: its row block's first row
+  // (row order), its group (quarter order) or its chain (eighth order).
   int r0 = L.w * kRowsPerWave;
-  if constexpr (Layout == 4) r0 += 2 * L.rgh;
+  if constexpr (Layout == 4) r0 = quarter_stage_pos(L.w, L.rgh, 0, 0);
   // The eighth layout's chain in the lane-ordered stage.
   if constexpr (Layout == 8) r0 = (L.w * kRowGroups + L.rg) * kRowsPerLane;
   // The head's gate constants, read once (a read per stage would wait on
@@ -645,7 +678,8 @@ __device__ __forceinline__ void prefill_tile(typename Storage<Tag>::T* __restric
     const int n = min(kStage, len - t0);
     // Every wave has finished reading the previous stage (the barrier at the
     // end of the stage loop), so it may be overwritten.
-    write_stage<kW, Layout == 8>(pre, L.wave, L.lane, gates, gc, n, st);
+    write_stage<kW, Layout == 8 ? kEighthOrder : (Layout == 4 ? kQuarterOrder : kRowOrder)>(
+        pre, L.wave, L.lane, gates, gc, n, st);
     __syncthreads();
     // The next stage's loads fly while this stage's tokens run.
     if (t0 + kStage < len)
