@@ -307,8 +307,13 @@ constexpr int kStage = 32;
 
 // Where row r of q_hat / k_hat sits in a stage vector, per layout:
 //   kRowOrder      r (the whole and split layouts read 32-row blocks);
-//   kEighthOrder   qk_lds_pos(r): an eighth-layout lane's chain of eight rows
-//                  is eight consecutive floats;
+//   kEighthOrder   an eighth-layout lane's chain of eight rows (row block w,
+//                  row group rg, i = 0..7) as two runs of four: i < 4 at
+//                  (w * 4 + rg) * 4 + i, i >= 4 at 64 + (w * 4 + rg) * 4 + i - 4,
+//                  so that a wave's 16-byte reads cover consecutive banks
+//                  (eight-float runs put a read's 16 chains on half the banks:
+//                  18-24 M bank-conflict cycles a launch; config 4 in this
+//                  layout 0.1616 -> 0.159 ms, the same bits);
 //   kQuarterOrder  a quarter-layout lane's 16 rows (row block w, row groups
 //                  2 rgh and 2 rgh + 1) are 16 consecutive floats, (i, rgl)
 //                  at 2 i + rgl, in groups of kQuarterGroup floats: the group
@@ -320,6 +325,9 @@ constexpr int kStage = 32;
 enum StageOrder { kRowOrder, kEighthOrder, kQuarterOrder };
 constexpr int kQuarterGroup = 20;
 constexpr int kStageVec = 8 * kQuarterGroup;  // >= kSS
+__device__ __forceinline__ int eighth_stage_pos(int w, int rg, int i) {
+  return (i >> 2) * 64 + (w * kRowGroups + rg) * 4 + (i & 3);
+}
 __device__ __forceinline__ int quarter_stage_pos(int w, int rgh, int i, int rgl) {
   return (w * 2 + rgh) * kQuarterGroup + 2 * i + rgl;
 }
@@ -447,11 +455,10 @@ __device__ __forceinline__ void write_stage(const StageRegs<kTileWaves>& r, int 
       } else if constexpr (kOrder == kEighthOrder) {
         // Rows e0 + k (e0 a multiple of 8): row block e0 / 32, row group k % 4,
         // chain index (e0 / 4) % 8 + k / 4.
-        const int base = (e0 >> 5) * (kRowGroups * kRowsPerLane) + ((e0 >> 2) & 7);
+        const int wb = e0 >> 5, i0 = (e0 >> 2) & 7;
         const float xs[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
-        for (int kk = 0; kk < 8; ++kk)
-          dst[base + (kk & 3) * kRowsPerLane + (kk >> 2)] = xs[kk] * fu;
+        for (int kk = 0; kk < 8; ++kk) dst[eighth_stage_pos(wb, kk & 3, i0 + (kk >> 2))] = xs[kk] * fu;
       } else {
         *reinterpret_cast<float4*>(dst + e0) = make_float4(a.x * fu, a.y * fu, a.z * fu, a.w * fu);
         *reinterpret_cast<float4*>(dst + e0 + 4) =
@@ -539,8 +546,21 @@ __device__ __forceinline__ void read_token_eighth(const StageLds& st, int j, int
   t.alpha = ab.x;
   t.beta = ab.y;
   t.v = st.v[j][col0];
-  loadN<kRowsPerLane>(&st.qk[j][1][pos], t.kh);
-  loadN<kRowsPerLane>(&st.qk[j][0][pos], t.qh);
+  float lo[4], hi[4];
+  loadN<4>(&st.qk[j][1][pos], lo);
+  loadN<4>(&st.qk[j][1][pos + 64], hi);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    t.kh[i] = lo[i];
+    t.kh[4 + i] = hi[i];
+  }
+  loadN<4>(&st.qk[j][0][pos], lo);
+  loadN<4>(&st.qk[j][0][pos + 64], hi);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    t.qh[i] = lo[i];
+    t.qh[4 + i] = hi[i];
+  }
 }
 
 // The eighth layout's state: the lane's chain, rows i = 2m and 2m + 1 in
@@ -667,7 +687,7 @@ __device__ __forceinline__ void prefill_tile(typename Storage<Tag>::T* __restric
   int r0 = L.w * kRowsPerWave;
   if constexpr (Layout == 4) r0 = quarter_stage_pos(L.w, L.rgh, 0, 0);
   // The eighth layout's chain in the lane-ordered stage.
-  if constexpr (Layout == 8) r0 = (L.w * kRowGroups + L.rg) * kRowsPerLane;
+  if constexpr (Layout == 8) r0 = eighth_stage_pos(L.w, L.rg, 0);
   // The head's gate constants, read once (a read per stage would wait on
   // memory in the middle of the prologue).
   const GateConst gc = gates.tile_consts(h);
