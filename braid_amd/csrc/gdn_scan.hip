@@ -819,6 +819,15 @@ __device__ __forceinline__ void prefill_tile(typename Storage<Tag>::T* __restric
   }
 }
 
+// A scan wave issues at most one VALU instruction per about five clocks and
+// waits on its own dependency chains between them, so its SIMD has issue
+// cycles to spare. A decode launched beside it (MixedTick: a memory-bound
+// launch on a side stream) shares those SIMDs; at the highest wave priority
+// the scan's instruction is the one chosen whenever it is ready, and the
+// decode issues in the cycles the scan leaves idle (config 4's tick, bucket
+// 96: 133.2 -> 129.3 us; a prefill alone is unchanged).
+__device__ __forceinline__ void raise_scan_priority() { __builtin_amdgcn_s_setprio(3); }
+
 // One tile (layout 2), a half tile (layout 1, kParts = 2), a quarter tile
 // (layout 4, kParts = 4) or an eighth (layout 8, kParts = 8) per workgroup:
 // blockIdx.x = (b * H + h) * kParts + part. Layouts 1, 4 and 8 run token
@@ -831,6 +840,7 @@ gdn_prefill_kernel(typename Storage<Tag>::T* __restrict__ pool,
                    const float* __restrict__ v, Gates gates, float* __restrict__ y,
                    int H, int G, int heads_per_group, int T) {
   using LM = typename ScanLayoutOf<Layout>::type;
+  raise_scan_priority();
   const int tile_id = blockIdx.x / LM::kParts;
   const int part = blockIdx.x - tile_id * LM::kParts;
   const int b = tile_id / H;
@@ -869,6 +879,7 @@ gdn_prefill_planned_kernel(typename Storage<Tag>::T* __restrict__ pool,
                            const float* __restrict__ v, Gates gates, float* __restrict__ y,
                            int B, int H, int G, int heads_per_group, int T, int cus,
                            int max_extra, int forced_plan) {
+  raise_scan_priority();
   __shared__ StageLds st;
   __shared__ int lens[kMaxPlanRows];
   __shared__ int order[kMaxPlanRows];  // row of each rank
