@@ -58,6 +58,12 @@ gdn_decode_kernel(typename Storage<Tag>::T* __restrict__ pool, const int* __rest
   using ST = typename Storage<Tag>::T;
   // Every argument in registers at once: one round of argument reads, not
   // one per first use.
+  // The loads are issued at the highest wave priority and the arithmetic at
+  // the lowest: a workgroup that starts while the CU's other workgroup is in
+  // its arithmetic then puts its tile's reads in flight first, before more of
+  // the other's VALU work (B = 128: 47.57 -> 47.32 us a step, bf16 and fp32
+  // pools about 1% faster, over three alternated runs each).
+  __builtin_amdgcn_s_setprio(3);
   pin_args(pool, slot_idx, q, k, v, y, H, heads_per_group, q_row, k_row, v_row, xcd_per);
   gates.pin_args();
   const int wg = stream_tile(xcd_per);
@@ -100,6 +106,7 @@ gdn_decode_kernel(typename Storage<Tag>::T* __restrict__ pool, const int* __rest
     load_qk2(L, qg, kg, q2, k2);
   }
   __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_setprio(0);
   // Every wave holds the gate inputs here, so their reads stay where they
   // were issued rather than moving into the wave that evaluates each gate.
   Gates::keep(gin);
