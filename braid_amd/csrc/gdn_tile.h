@@ -356,29 +356,6 @@ __device__ __forceinline__ float add_xor32(float v) {
   return __uint_as_float(p[0]) + __uint_as_float(p[1]);
 }
 
-// The same partner sums where only the lower lanes of each pair consume the
-// result: lanes of even 16-lane rows (xor 16) or of the lower 32 lanes (xor
-// 32) end with v + partner, the same addition in the same operand order as
-// add_xor16 / add_xor32, so the same bits there; the other lanes hold
-// garbage. The swap's second operand is a don't-care register, so the
-// compiler need not copy v into it first (each full-wave swap of v with
-// itself costs a v_mov and a wait state).
-// A register with no defined value: an empty asm that "writes" it, so the
-// compiler emits nothing to set it (a poison value would be set to 0).
-__device__ __forceinline__ uint32_t dont_care() {
-  uint32_t x;
-  asm volatile("" : "=v"(x));
-  return x;
-}
-__device__ __forceinline__ float add_xor16_lo(float v) {
-  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), dont_care(), false, false);
-  return __uint_as_float(p[0]) + __uint_as_float(p[1]);
-}
-__device__ __forceinline__ float add_xor32_lo(float v) {
-  const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), dont_care(), false, false);
-  return __uint_as_float(p[0]) + __uint_as_float(p[1]);
-}
-
 // Sum over all 64 lanes: stages xor 1, 2, 4, 8, 16, 32.
 __device__ __forceinline__ float wave_sum(float v) {
   return add_xor32(add_xor16(add_xor8(add_xor4(add_xor2(add_xor1(v))))));
@@ -388,10 +365,10 @@ __device__ __forceinline__ float wave_sum(float v) {
 // v + (lane xor 16), then + (lane xor 32). kPermlane: through the permlane
 // swaps (VALU); otherwise through ds_bpermute, which holds no extra registers
 // (the fused conv + decode kernels have none to spare at 128 VGPRs). Same
-// sums either way (a + b == b + a), so the same bits. (The lower-lanes
-// variants add_xor*_lo would do here too, since only row group 0 stores the
-// totals; measured on the B = 128 decode they gained nothing, 47.96 -> 48.00
-// us, so the full-wave swaps stay.)
+// sums either way (a + b == b + a), so the same bits. (Swaps of v against a
+// don't-care register, valid only in row group 0's lanes, which alone store
+// the totals, saved a copy per stage but gained nothing on the B = 128
+// decode, 47.96 -> 48.00 us, so the full-wave swaps stay.)
 template <bool kPermlane = false>
 __device__ __forceinline__ float rowgroup_sum(float v) {
   if constexpr (kPermlane) return add_xor32(add_xor16(v));
@@ -753,11 +730,12 @@ struct ScanMap {
 
 // Quarter scan layout: one column and two of the four row groups per lane, so
 // a lane holds 16 rows and a tile spreads over four workgroups of four waves
-// (8 columns per wave). Lane l: column cc = l % 8, row-group half
-// rgh = (l / 8) % 2 (row groups 2 rgh and 2 rgh + 1), row block w = l / 16.
-// Column totals: in-lane (rg 2rgh + rg 2rgh+1), then lane xor 8 gives
-// (rg0 + rg1) + (rg2 + rg3), then xor 16 and xor 32 as in the other layouts,
-// which is the decode's order.
+// (8 columns per wave). Lane l: row-group half rgh = l % 2 (row groups 2 rgh
+// and 2 rgh + 1), row block w = (l / 2) % 4, column cc = l / 8. Column totals:
+// in-lane (rg 2rgh + rg 2rgh+1), then lane xor 1 gives (rg0 + rg1) + (rg2 + rg3),
+// then xor 2 and xor 4 give (w0 + w1) + (w2 + w3): the decode's order, every
+// exchange a DPP stage inside a 16-lane row (no permlane swap; config 4's
+// 4 x 256 tokens in this layout 0.1197 -> 0.1163 ms, the same bits).
 struct ScanMapQuarter {
   static constexpr int kCPL = 1;
   static constexpr int kLaneRowGroups = 2;
@@ -769,9 +747,9 @@ struct ScanMapQuarter {
   __device__ __forceinline__ ScanMapQuarter(int tid, int part) {
     lane = tid & 63;
     wave = tid >> 6;
-    cc = lane & 7;
-    rgh = (lane >> 3) & 1;
-    w = lane >> 4;
+    rgh = lane & 1;
+    w = (lane >> 1) & 3;
+    cc = lane >> 3;
     col0 = (part * kWaves + wave) * kColsPerWave + cc;
   }
   // rgl: the lane's row group 0 or 1 (row group 2 rgh + rgl).
@@ -1151,7 +1129,7 @@ __device__ __forceinline__ void scan_token_quarter(RowPair1<Tag> (&P)[kRowsPerLa
 #pragma unroll
     for (int i = 1; i < kRowsPerLane; ++i) ch[g] = fmaf(P[i].get(g), kh[g][i], ch[g]);
   }
-  const float kv = add_xor32(add_xor16(add_xor8(ch[0] + ch[1])));
+  const float kv = add_xor4(add_xor2(add_xor1(ch[0] + ch[1])));
   const float delta = (v - alpha * kv) * beta;
   ch[0] = ch[1] = 0.f;
 #pragma unroll
@@ -1166,7 +1144,7 @@ __device__ __forceinline__ void scan_token_quarter(RowPair1<Tag> (&P)[kRowsPerLa
 #pragma unroll
     for (int g = 0; g < 2; ++g) ch[g] = fmaf(n[g], qh[g][i], ch[g]);
   }
-  y = add_xor32_lo(add_xor16_lo(add_xor8(ch[0] + ch[1]))) * kYScale;
+  y = add_xor4(add_xor2(add_xor1(ch[0] + ch[1]))) * kYScale;
 }
 
 // One token of the eighth layout on this lane's chain of 8 rows x 1 column:
