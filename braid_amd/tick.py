@@ -9,7 +9,13 @@ kernels overlap: the prefill scan is a latency-bound serial chain (one
 workgroup per CU at a tick's sizes), and the decode, a memory stream, fills the
 CUs' remaining issue slots and the HBM beside it. On MI355X (config 4: 96
 decode rows + 4 x 256 prefill tokens, fp16 pool, graph-replayed) the tick takes
-131.5 us against 158 us in sequence; the prefill alone takes 121 us.
+129 us against 156 us in sequence; the prefill alone takes 119 us.
+
+The prefill is captured first, and that order matters: the graph's branches
+start in capture order, and a large decode asks for enough LDS to hold two of
+its workgroups per CU, so a decode that started first would keep the prefill's
+workgroups off the CUs until it drained (measured: 205 us for the tick with the
+decode captured first).
 
 The two launches touch disjoint slots (the decode takes only rows that are no
 longer prefilling, scheduler.py:267), so their order does not change a bit:
@@ -83,6 +89,8 @@ class MixedTick:
                                f"the pool on {pool.device}")
         main = torch.cuda.current_stream(pool.device)
         self.side.wait_stream(main)
+        # The prefill first (see the module docstring): its workgroups must
+        # hold their CUs before the decode's arrive.
         self.kern.gdn_prefill_raw(pool, *pre, **plan)
         with torch.cuda.stream(self.side):
             self.kern.gdn_decode_raw(pool, *dec)
