@@ -3,7 +3,7 @@
 // share it, so the probe keeps streaming exactly what the decode streams.
 //
 // Two measured choices (MI355X: 256 CUs in 8 XCDs, cold slot-permuted pools),
-// both taken only for a "large" launch: at least 8 tiles per CU for 16-bit
+// both taken only for a "large" launch: at least 6 tiles per CU for 16-bit
 // tiles, 12 for fp32 tiles.
 //
 // * XCD-contiguous tiles. The dispatcher deals consecutive workgroups to the
@@ -21,7 +21,11 @@
 //   96: 37.6 / 37.4-37.6 / 38.1 / 38.1 us. With the decode built for two
 //   waves per SIMD at this cap (gdn_scan.hip), remap + cap 2 against neither:
 //   B = 80 32.4 -> 31.2 us, B = 64 26.2 -> 25.9, B = 48 20.25 -> 20.3, B = 32
-//   13.8 -> 14.8; hence 8 tiles per CU. fp32 tiles (64 KiB, large from 12
+//   13.8 -> 14.8. Once the decode issued its loads at the highest wave
+//   priority (gdn_scan.hip), B = 48 (6 tiles per CU) joined: default 21.6,
+//   remap + cap 2 20.3 us; B = 40 (5 per CU) is the same either way and B =
+//   32 is slower capped (15.0 against 12.0); hence 6 tiles per CU. fp32
+//   tiles (64 KiB, large from 12
 //   tiles per CU) take the cap too: cap 2 / 3 / none at B = 96, 128, 192, 256:
 //   70.0 / 70.5 / 70.9, 91.8 / 92.5 / 93.4, 134.7 / 136.9 / 138.2, 178.1 /
 //   181.6 / 183.3 us.
@@ -114,7 +118,7 @@ inline int env_int(const char* name) {
 // LDS per CU.
 inline StreamShape stream_shape(long n_tiles, const DeviceTopo& topo, bool narrow,
                                 size_t static_lds, int remap_env = -1, int cap_env = -1) {
-  const bool large = topo.cus > 0 && n_tiles >= (narrow ? 8L : 12L) * topo.cus;
+  const bool large = topo.cus > 0 && n_tiles >= (narrow ? 6L : 12L) * topo.cus;
   StreamShape s{0, 0};
   const bool remap = remap_env >= 0 ? remap_env > 0 : (large && topo.xcds == kXcds);
   s.xcd_per = (remap && n_tiles % kXcds == 0) ? (int)(n_tiles / kXcds) : 0;

@@ -3,7 +3,7 @@ topologies, on the CPU: a host-only program compiled with hipcc calls
 stream_shape() with synthetic DeviceTopo values (no HIP runtime call), so a
 partitioned device or an unknown one can be checked without the hardware.
 
-A large launch (>= 8 tiles per CU for 16-bit tiles, 12 for fp32) takes the
+A large launch (>= 6 tiles per CU for 16-bit tiles, 12 for fp32) takes the
 two-per-CU residency cap, the device's LDS per CU halved, less the kernel's
 own LDS and 1 KiB, at most 64 KiB, and, only on a device with 8 XCDs and a
 tile count divisible by 8, the XCD-contiguous order (per = tiles / 8)."""
@@ -29,6 +29,8 @@ int main() {
       unknown{};
   show("full_b128", stream_shape(4096, full, true, 8704));
   show("full_b64", stream_shape(2048, full, true, 8704));
+  show("full_b48", stream_shape(1536, full, true, 8704));
+  show("full_b40", stream_shape(1280, full, true, 8704));
   show("full_b32", stream_shape(1024, full, true, 8704));
   show("full_f32_b64", stream_shape(2048, full, false, 8704));
   show("full_f32_b96", stream_shape(3072, full, false, 8704));
@@ -61,7 +63,10 @@ def test_a_whole_mi355x_takes_the_measured_shape(shapes):
     # B = 128 and B = 64 at 32 heads: 16 and 8 tiles per CU on 256 CUs
     assert shapes["full_b128"] == (512, 65536)
     assert shapes["full_b64"] == (256, 65536)
-    # 4 tiles per CU: neither choice
+    # B = 48: 6 tiles per CU, the smallest large launch
+    assert shapes["full_b48"] == (192, 65536)
+    # 5 and 4 tiles per CU: neither choice
+    assert shapes["full_b40"] == (0, 0)
     assert shapes["full_b32"] == (0, 0)
     # fp32 tiles are large from 12 per CU
     assert shapes["full_f32_b64"] == (0, 0)
