@@ -44,8 +44,9 @@ BASELINE shapes, each captured in a hipGraph and timed with events:
   quantize_act      [64, 4096] bf16 (both launches)
   readout_quant_*   gated RMSNorm readout + out_proj input FP8 quant (both
                     launches), 64 decode tokens and config 2's 4073 tokens
-  fp8_gemm_*        config 3's FP8 projection GEMMs at B=64 through hipBLASLt
-                    (bytes: fp8 weight + x + bf16 out), torch._scaled_mm beside
+  fp8_gemm_*        config 3's FP8 projection GEMMs at B=64, streaming kernel
+                    (bytes: fp8 weight + x + bf16 out), weights cycled through
+                    HBM; hipBLASLt and torch._scaled_mm beside it
   mixer_step        config 3: 24 GDN layers of quant -> conv -> gated decode at
                     B=64, one fp16 pool and conv pool per layer
   mixer_step_fused  the same step with conv + decode fused in one launch
@@ -583,23 +584,46 @@ def measure_paths(torch, kern):
                       "hbm_frac": round(rbytes / t / 1e9 / HBM_PEAK_GBS, 4)}
         del ry, rz
 
-    # FP8 projection GEMMs of config 3's layer at B=64 (hipBLASLt): in_proj
-    # qkv + z (N = 8192 + 4096) and out_proj (N = 4096), K = 4096; HBM-bound
-    # on the fp8 weight bytes
+    # FP8 projection GEMMs of config 3's layer at B=64 (the streaming kernel):
+    # in_proj qkv + z (N = 8192 + 4096) and out_proj (N = 4096), K = 4096;
+    # HBM-bound on the fp8 weight bytes. `us` cycles through distinct weights
+    # totalling >= 512 MB, so each call reads its weight from HBM as a model's
+    # layers do (one weight timed over and over stays in the 256 MB MALL:
+    # `us_mall_resident`). hipBLASLt (the library path, BRAID_FP8_GEMM=0) and
+    # torch._scaled_mm, the reference's call, are timed the same two ways.
     xg = torch.randn(64, 4096, generator=g, device=dev).to(torch.bfloat16)
     xgq, sxg = kern.quantize_act(xg)
     for label, N in (("fp8_gemm_in_proj_b64", 12288), ("fp8_gemm_out_proj_b64", 4096)):
-        wq, sw = kern.quantize_act(torch.randn(N, 4096, generator=g, device=dev) * 0.02)
-        t = graph_time(torch, lambda: kern.fp8_matmul(xgq, sxg, wq, sw), reps=11, inner=20)
-        t_ref = graph_time(torch, lambda: torch._scaled_mm(xgq, wq.t(), scale_a=sxg, scale_b=sw,
-                                                           out_dtype=torch.bfloat16),
-                           reps=11, inner=20)
+        n_w = -(-(512 << 20) // (N * 4096))
+        ws = [kern.quantize_act(torch.randn(N, 4096, generator=g, device=dev) * 0.02)
+              for _ in range(n_w)]
+
+        def cycle(fn):
+            def run():
+                for wq, sw in ws:
+                    fn(wq, sw)
+            return run
+
+        ours = lambda wq, sw: kern.fp8_matmul(xgq, sxg, wq, sw)  # noqa: E731
+        ref = lambda wq, sw: torch._scaled_mm(xgq, wq.t(), scale_a=sxg, scale_b=sw,  # noqa: E731
+                                              out_dtype=torch.bfloat16)
+        t = graph_time(torch, cycle(ours), reps=11, inner=2) / n_w
+        t_res = graph_time(torch, lambda: ours(*ws[0]), reps=11, inner=20)
+        with kern.launch_override(fp8_gemm=0):
+            t_lib = graph_time(torch, cycle(ours), reps=11, inner=2) / n_w
+            t_lib_res = graph_time(torch, lambda: ours(*ws[0]), reps=11, inner=20)
+        t_ref = graph_time(torch, cycle(ref), reps=11, inner=2) / n_w
+        t_ref_res = graph_time(torch, lambda: ref(*ws[0]), reps=11, inner=20)
         gbytes = N * 4096 + 64 * 4096 + 64 * N * 2
-        out[label] = {"shape": f"M=64 N={N} K=4096", "us": round(t * 1e6, 2),
-                      "gbs": round(gbytes / t / 1e9, 1),
+        out[label] = {"shape": f"M=64 N={N} K=4096", "weights_cycled": n_w,
+                      "us": round(t * 1e6, 2), "gbs": round(gbytes / t / 1e9, 1),
                       "hbm_frac": round(gbytes / t / 1e9 / HBM_PEAK_GBS, 4),
-                      "torch_scaled_mm_us": round(t_ref * 1e6, 2)}
-        del wq
+                      "us_mall_resident": round(t_res * 1e6, 2),
+                      "hipblaslt_us": round(t_lib * 1e6, 2),
+                      "hipblaslt_us_mall_resident": round(t_lib_res * 1e6, 2),
+                      "torch_scaled_mm_us": round(t_ref * 1e6, 2),
+                      "torch_scaled_mm_us_mall_resident": round(t_ref_res * 1e6, 2)}
+        del ws
 
     # config 3: 24-layer mixer decode step at B=64
     L, Bm, S = 24, 64, 72

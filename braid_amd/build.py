@@ -34,7 +34,7 @@ PROBE_SOURCE = "hbm_probe.hip"
 OBJ_DIR = PKG / "_build"
 
 SOURCES = ["capi_common.cpp", "gdn_scan.hip", "conv1d_decode.hip", "quant_act.hip",
-           "gated_norm.hip", "fp8_gemm.cpp"]
+           "gated_norm.hip", "fp8_gemm.cpp", "fp8_gemm_stream.hip"]
 # hipBLASLt for the FP8 GEMM. Its SONAME (libhipblaslt.so.1) matches the copy
 # torch loads, so in a torch process the library binds to that one.
 LIBS = ["-L/opt/rocm/lib", "-lhipblaslt"]

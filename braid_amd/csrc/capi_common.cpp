@@ -24,10 +24,10 @@ int parse_knob(const char* e) {
 
 namespace {
 
-constexpr int kKnobs = 5;
+constexpr int kKnobs = 6;
 const char* const kKnobEnv[kKnobs] = {"BRAID_DECODE_XCD_REMAP", "BRAID_DECODE_WGS_PER_CU",
                                       "BRAID_PREFILL_COLS", "BRAID_DECODE_PARTS",
-                                      "BRAID_PREFILL_PLAN"};
+                                      "BRAID_PREFILL_PLAN", "BRAID_FP8_GEMM"};
 
 // Read once, at library load (static initialisation), not per launch. A value
 // that is not a whole decimal number in [0, 2^30], or is empty, leaves the

@@ -36,7 +36,7 @@ int validate_slots(const int32_t* slot_idx, int B, int64_t n_slots, bool distinc
 // Launch knobs, for measurement: overrides of the launch-shape choices,
 // -1 when unset. Initialised once from the environment when the library
 // loads (BRAID_DECODE_XCD_REMAP, BRAID_DECODE_WGS_PER_CU, BRAID_PREFILL_COLS,
-// BRAID_DECODE_PARTS, BRAID_PREFILL_PLAN), then changed only by
+// BRAID_DECODE_PARTS, BRAID_PREFILL_PLAN, BRAID_FP8_GEMM), then changed only by
 // braid_set_launch_override. The knobs are process-wide: an override set on
 // one thread shapes the launches of every thread.
 int launch_knob(int knob);

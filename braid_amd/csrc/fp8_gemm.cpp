@@ -1,11 +1,15 @@
-// FP8 (e4m3fn) W8A8 GEMM with per-tensor dequant scales, through hipBLASLt.
+// FP8 (e4m3fn) W8A8 GEMM with per-tensor dequant scales: decode shapes on
+// the hand-written streaming kernel (fp8_gemm_stream.hip), the rest through
+// hipBLASLt.
 //
 // Reference behaviour: braid/model/quant.py:232-241 (`fp8_matmul`), which calls
 //   torch._scaled_mm(xq, w.data.t(), scale_a=sx, scale_b=w.scale, out_dtype)
 //   out[M, N] = (xq[M, K] * sx) @ (w[N, K] * sw)^T
-// with fp32 accumulation. This is a plain library GEMM, so it goes to
-// hipBLASLt rather than a hand-written kernel; the decode-time shapes (M = the
-// batch, N x K = a projection's weight) are weight-streaming bound.
+// with fp32 accumulation. At decode shapes (M = the batch, at most 64; N x K =
+// a projection's weight) the GEMM is weight-streaming bound, and the
+// streaming kernel reads the weight at a higher rate than the library's
+// tiles (its coalesced loads and one column block per CU over the whole of
+// K); larger M is a plain library GEMM.
 //
 // hipBLASLt is column-major. The row-major operands read column-major are
 // w^T [K, N] and xq^T [K, M]; with op(A) = T on A = w and op(B) = N on B = xq,
@@ -23,6 +27,7 @@
 #include <tuple>
 
 #include "capi_common.h"
+#include "fp8_gemm_stream.h"
 
 namespace braid {
 namespace {
@@ -119,6 +124,12 @@ extern "C" int braid_fp8_gemm(const uint8_t* x, const float* x_scale, const uint
     return fail(BRAID_EINVAL, "x/x_scale/w/w_scale/out/workspace must be non-null");
   if (!aligned16(x) || !aligned16(w) || !aligned16(out) || !aligned16(workspace))
     return fail(BRAID_EINVAL, "x, w, out and workspace must be 16-byte aligned");
+  // Decode shapes (M <= 64) stream the weight through the hand-written
+  // kernel; the rest, and BRAID_FP8_GEMM=0, go to hipBLASLt.
+  if (launch_knob(BRAID_KNOB_FP8_GEMM) != 0 && fp8_gemm_stream_fits(M, N, K)) {
+    const int st = fp8_gemm_stream(x, x_scale, w, w_scale, out, out_dtype, M, N, K, stream);
+    return st ? st : ok();
+  }
   int dev = 0;
   int st;
   if ((st = hip_status(hipGetDevice(&dev), "hipGetDevice"))) return st;

@@ -185,13 +185,14 @@ class GDNKernels:
     # -- launch knobs (measurement / tests) ------------------------------------
 
     KNOBS = {"decode_xcd_remap": 0, "decode_wgs_per_cu": 1, "prefill_layout": 2,
-             "decode_parts": 3, "prefill_plan": 4}
+             "decode_parts": 3, "prefill_plan": 4, "fp8_gemm": 5}
 
     @contextlib.contextmanager
     def launch_override(self, **knobs):
         """Force launch-shape choices for the calls inside the block (None:
         the library's own choice), restoring the previous values after. Only
-        the time changes; every shape gives the same bits."""
+        the time changes; every shape gives the same bits, except fp8_gemm,
+        which picks between two GEMMs that sum in different orders."""
         prev = {}
         try:
             for name, val in knobs.items():

@@ -65,6 +65,8 @@ const char* braid_last_error(void);
  *                                a planned prefill runs its n8 longest rows in the
  *                                eighth layout, the next n4 quarter, the next n2
  *                                split
+ *   BRAID_KNOB_FP8_GEMM          (BRAID_FP8_GEMM)          0 hipBLASLt, 1 the streaming
+ *                                small-M kernel (where its shape rules allow)
  *
  * A captured graph keeps the launch shape it was captured with. An environment
  * value that is not a whole decimal number in [0, 2^30] leaves the knob unset.
@@ -77,6 +79,7 @@ enum braid_launch_knob {
   BRAID_KNOB_PREFILL_LAYOUT = 2,
   BRAID_KNOB_DECODE_PARTS = 3,
   BRAID_KNOB_PREFILL_PLAN = 4,
+  BRAID_KNOB_FP8_GEMM = 5,
 };
 /*
  * The plan an eager braid_gdn_prefill_raw with seq_lens chooses for a ragged
@@ -318,7 +321,11 @@ int braid_gated_rmsnorm_quant(const void* y, int y_dtype, const void* z,
 size_t braid_fp8_gemm_workspace(void);
 
 /*
- * FP8 e4m3fn W8A8 GEMM with per-tensor dequant scales, through hipBLASLt.
+ * FP8 e4m3fn W8A8 GEMM with per-tensor dequant scales. Decode shapes
+ * (1 <= M <= 64, K = 1024 * 2^i for i < 5) run a hand-written kernel that
+ * streams the weight once (no workspace used, fixed summation order, so
+ * repeated calls give the same bits); other shapes, and every shape under
+ * BRAID_FP8_GEMM=0, run one hipBLASLt matmul.
  * Replaces fp8_matmul's torch._scaled_mm(xq, w.t(), scale_a=sx, scale_b=sw)
  * (braid/model/quant.py:232-241).
  *
@@ -329,8 +336,10 @@ size_t braid_fp8_gemm_workspace(void);
  *   out      [M, N] of out_dtype (BRAID_BF16, F16 or F32), row-major:
  *            out = (x * x_scale) @ (w * w_scale)^T, fp32 accumulation
  *   workspace  device scratch of workspace_bytes (>= braid_fp8_gemm_workspace())
- * N and K must be multiples of 16. The first call for a shape selects the
- * algorithm on the host; later calls only enqueue, and may be captured.
+ * N and K must be multiples of 16. On the hipBLASLt path the first call for a
+ * shape selects the algorithm on the host; later calls only enqueue, and may
+ * be captured (the streaming kernel needs no such first call). Calls sharing
+ * one workspace must not overlap.
  */
 int braid_fp8_gemm(const uint8_t* x, const float* x_scale, const uint8_t* w,
                    const float* w_scale, void* out, int out_dtype, int64_t M,

@@ -271,10 +271,11 @@ def test_launch_knobs_ignore_malformed_environment_values():
     code = (
         "import ctypes, sys; from braid_amd.kernels import loader; "
         "lib = ctypes.CDLL(str(loader.LIB_PATH)); "
-        "print(' '.join(str(lib.braid_get_launch_override(i)) for i in range(5)))"
+        "print(' '.join(str(lib.braid_get_launch_override(i)) for i in range(6)))"
     )
     env = dict(os.environ, BRAID_DECODE_XCD_REMAP="abc", BRAID_DECODE_WGS_PER_CU="2x",
-               BRAID_PREFILL_COLS="", BRAID_DECODE_PARTS="-2", BRAID_PREFILL_PLAN="1025")
+               BRAID_PREFILL_COLS="", BRAID_DECODE_PARTS="-2", BRAID_PREFILL_PLAN="1025",
+               BRAID_FP8_GEMM="0")
     out = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True,
                          cwd=str(Path(__file__).resolve().parents[1]), check=True)
-    assert out.stdout.split() == ["-1", "-1", "-1", "-1", "1025"], out.stdout + out.stderr
+    assert out.stdout.split() == ["-1", "-1", "-1", "-1", "1025", "0"], out.stdout + out.stderr

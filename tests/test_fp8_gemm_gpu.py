@@ -1,12 +1,14 @@
-"""FP8 W8A8 GEMM (hipBLASLt through braid_fp8_gemm) on the GPU.
+"""FP8 W8A8 GEMM (braid_fp8_gemm: the streaming kernel at decode shapes,
+hipBLASLt otherwise) on the GPU.
 
 Reference: braid/model/quant.py:232-289 (fp8_matmul = torch._scaled_mm with
 per-tensor scales; fp8_linear / project quantize the activation once).
 The FP8 products are exact in fp32 and only the accumulation order is the
-library's, so the output is checked against an fp32 reference of the same
+kernel's, so the output is checked against an fp32 reference of the same
 dequantized operands: within one unit of the output dtype's rounding plus a
-fp32 accumulation allowance. It is also checked against torch._scaled_mm on
-this device, the reference's own call.
+fp32 accumulation allowance, on both paths (the launch knob forces
+hipBLASLt). It is also checked against torch._scaled_mm on this device, the
+reference's own call.
 """
 from __future__ import annotations
 
@@ -15,6 +17,7 @@ import torch
 
 from braid_amd.quant import (FP8Weight, fp8_linear, fp8_matmul, linear, project,
                              quantize_act, quantize_weight)
+from braid_amd.kernels.loader import load_gdn
 from gpu_helpers import DEV, gen
 
 pytestmark = pytest.mark.gpu
@@ -33,17 +36,50 @@ def _check(out, ref, dt, K):
     assert bool((err <= tol).all()), f"max excess {(err - tol).max().item():.3e}"
 
 
+PATHS = {"default": None, "hipblaslt": 0}
+
+
+@pytest.mark.parametrize("path", list(PATHS))
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16, torch.float32],
                          ids=["bf16", "fp16", "fp32"])
 @pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (64, 12288, 4096), (37, 4096, 4096),
                                    (64, 4096, 4096), (128, 1024, 2048)])
-def test_matches_the_fp32_reference(M, N, K, dt):
+def test_matches_the_fp32_reference(M, N, K, dt, path):
     x = torch.randn(M, K, generator=gen(M + N), device=DEV).to(dt)
     w = quantize_weight(torch.randn(N, K, generator=gen(K), device=DEV) * 0.02)
     xq, sx = quantize_act(x)
-    out = fp8_matmul(xq, sx, w, out_dtype=dt)
+    with load_gdn().launch_override(fp8_gemm=PATHS[path]):
+        out = fp8_matmul(xq, sx, w, out_dtype=dt)
     assert out.dtype == dt and tuple(out.shape) == (M, N)
     _check(out, _ref(xq, sx, w), dt, K)
+
+
+# the streaming kernel's edges: one workgroup (N = 16), every partial 16-row
+# block (M = 17, 33, 49), 1 and 16 k-steps per wave (K = 1024, 16384), a
+# column count that is no multiple of 48 or 32; and shapes it leaves to
+# hipBLASLt (M = 65; K not 1024 * 2^i)
+@pytest.mark.parametrize("M,N,K", [(1, 16, 1024), (17, 48, 2048), (33, 4112, 1024),
+                                   (49, 1024, 16384), (64, 272, 8192), (65, 512, 1024),
+                                   (8, 512, 3072)])
+def test_stream_kernel_edges(M, N, K):
+    x = torch.randn(M, K, generator=gen(3 * M + N), device=DEV).bfloat16()
+    w = quantize_weight(torch.randn(N, K, generator=gen(K + 1), device=DEV) * 0.02)
+    xq, sx = quantize_act(x)
+    for dt in (torch.bfloat16, torch.float32):
+        _check(fp8_matmul(xq, sx, w, out_dtype=dt), _ref(xq, sx, w), dt, K)
+
+
+def test_stream_kernel_is_deterministic_and_agrees_with_hipblaslt():
+    x = torch.randn(64, 4096, generator=gen(21), device=DEV).bfloat16()
+    w = quantize_weight(torch.randn(12288, 4096, generator=gen(22), device=DEV) * 0.02)
+    xq, sx = quantize_act(x)
+    a = fp8_matmul(xq, sx, w, out_dtype=torch.float32)
+    b = fp8_matmul(xq, sx, w, out_dtype=torch.float32)
+    assert torch.equal(a, b)
+    with load_gdn().launch_override(fp8_gemm=0):
+        lib = fp8_matmul(xq, sx, w, out_dtype=torch.float32)
+    # two fp32 summation orders of the same exact products
+    assert bool(((a - lib).abs() <= 1e-5 * a.abs().max()).all())
 
 
 @pytest.mark.parametrize("M,N,K", [(16, 4096, 4096), (64, 12288, 4096)])
